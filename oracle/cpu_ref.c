@@ -1,0 +1,554 @@
+/*
+ * oracle/cpu_ref.c — CPU restatement of vib3's MoE expert path. TEST INFRASTRUCTURE ONLY:
+ * the HIP product never links or calls this file; tests/ and bench.py's cpu_baseline leg do.
+ *
+ * Built with -O2 -ffp-contract=off (see oracle/Makefile) so that every `acc += a * b` is a
+ * rounded multiply followed by a rounded add, exactly as rustc compiles the reference loops
+ * (Rust never contracts a*b+c into an FMA). Row parallelism (rayon in the reference,
+ * kernels.rs:2658 PARALLEL_ROW_THRESHOLD = 64) only changes which thread computes a row,
+ * never the arithmetic, so pthreads over row ranges reproduce it.
+ */
+#include "cpu_ref.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+/* ------------------------------------------------------------------ conversions */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* f32 -> f16, round to nearest even, subnormals and overflow to inf, NaN kept quiet. */
+uint16_t v3o_f32_to_f16(float f)
+{
+    uint32_t x = f2u(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (exp == 0xff) {
+        if (man == 0) return (uint16_t)(sign | 0x7c00u);
+        return (uint16_t)(sign | 0x7e00u | (man >> 13));
+    }
+    int e = (int)exp - 127 + 15;
+    if (e >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        /* subnormal half: value = man24 * 2^(exp-150); half quantum 2^-24 */
+        if (e < -10) return (uint16_t)sign; /* below half of the smallest subnormal */
+        uint32_t m = man | 0x800000u;       /* 24-bit significand */
+        uint32_t shift = (uint32_t)(14 - e); /* bits to drop: 13 + (1 - e) */
+        uint32_t half_m = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t halfway = 1u << (shift - 1u);
+        if (rem > halfway || (rem == halfway && (half_m & 1u))) half_m++;
+        return (uint16_t)(sign | half_m);
+    }
+    uint32_t half_m = man >> 13;
+    uint32_t rem = man & 0x1fffu;
+    uint32_t out = sign | ((uint32_t)e << 10) | half_m;
+    if (rem > 0x1000u || (rem == 0x1000u && (half_m & 1u))) out++; /* carries into exp ok */
+    return (uint16_t)out;
+}
+
+float v3o_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    if (exp == 0) {
+        if (man == 0) return u2f(sign);
+        /* subnormal: man * 2^-24 exactly */
+        float v = (float)man * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    if (exp == 0x1f) return u2f(sign | 0x7f800000u | (man << 13));
+    return u2f(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+/* half::bf16::from_f32: NaN -> quiet NaN of the top bits, otherwise round to nearest even. */
+uint16_t v3o_f32_to_bf16(float f)
+{
+    uint32_t x = f2u(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u);
+    uint32_t round_bit = 0x8000u;
+    if ((x & round_bit) != 0 && (x & (3u * round_bit - 1u)) != 0) return (uint16_t)((x >> 16) + 1u);
+    return (uint16_t)(x >> 16);
+}
+
+float v3o_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+void v3o_to_f32(const void *src, int dt, size_t n, float *dst)
+{
+    if (dt == V3O_F32) { memcpy(dst, src, n * 4); return; }
+    const uint16_t *s = (const uint16_t *)src;
+    for (size_t i = 0; i < n; i++)
+        dst[i] = dt == V3O_F16 ? v3o_f16_to_f32(s[i]) : v3o_bf16_to_f32(s[i]);
+}
+
+static inline float decode_scale(const uint8_t *p, int dt)
+{
+    uint16_t bits = (uint16_t)(p[0] | (p[1] << 8));
+    return dt == V3O_F16 ? v3o_f16_to_f32(bits) : v3o_bf16_to_f32(bits);
+}
+
+/* kernels.rs:2789-2797: a scale that is not finite or not > 0 decodes as 1/8. */
+static inline float valid_scale(float s) { return (isfinite(s) && s > 0.0f) ? s : 0.125f; }
+
+/* ------------------------------------------------------------------ threading */
+
+int v3o_default_threads(void)
+{
+    const char *env = getenv("VIB3_ORACLE_THREADS");
+    if (env && atoi(env) > 0) return atoi(env);
+    long n = sysconf(_SC_NPROCESSORS_ONLN);
+    return n > 0 ? (int)n : 1;
+}
+
+typedef void (*row_fn)(void *ctx, size_t r0, size_t r1);
+typedef struct { row_fn fn; void *ctx; size_t r0, r1; } row_job;
+
+static void *row_thread(void *p)
+{
+    row_job *j = (row_job *)p;
+    j->fn(j->ctx, j->r0, j->r1);
+    return NULL;
+}
+
+/* Run fn over [0, m) split into contiguous ranges; sequential below 64 rows like the
+ * reference (kernels.rs:2658). */
+static void parallel_rows(size_t m, int nthreads, row_fn fn, void *ctx)
+{
+    if (nthreads <= 0) nthreads = v3o_default_threads();
+    if (m < 64 || nthreads == 1) { fn(ctx, 0, m); return; }
+    if ((size_t)nthreads > m) nthreads = (int)m;
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nthreads);
+    row_job *jobs = (row_job *)malloc(sizeof(row_job) * (size_t)nthreads);
+    size_t per = (m + (size_t)nthreads - 1) / (size_t)nthreads;
+    int started = 0;
+    for (int t = 0; t < nthreads; t++) {
+        size_t r0 = (size_t)t * per, r1 = r0 + per > m ? m : r0 + per;
+        if (r0 >= r1) break;
+        jobs[t] = (row_job){fn, ctx, r0, r1};
+        if (pthread_create(&th[t], NULL, row_thread, &jobs[t]) != 0) { fn(ctx, r0, r1); continue; }
+        started = t + 1;
+    }
+    for (int t = 0; t < started; t++) pthread_join(th[t], NULL);
+    free(th);
+    free(jobs);
+}
+
+/* ------------------------------------------------------------------ INT4 GEMV */
+
+typedef struct {
+    const float *x;
+    const uint8_t *page;
+    size_t k, m, g;
+    int sdt;
+    float *acc;
+} int4_ctx;
+
+/* One row of cpu_matmul_int4_grouped (kernels.rs:2770-2820): build the 16-entry LUT per group,
+ * then the byte loop: acc += x[col] * lut[lo]; acc += x[col+1] * lut[hi]. */
+static float int4_row(const float *x, const uint8_t *page, size_t k, size_t m, size_t g, int sdt,
+                      size_t row, float *lut /* [G*16] */)
+{
+    size_t pk = (k + 1) / 2, ng = (k + g - 1) / g;
+    const uint8_t *rowp = page + row * pk;
+    const uint8_t *sc = page + pk * m + row * ng * 2;
+    for (size_t gi = 0; gi < ng; gi++) {
+        float s = valid_scale(decode_scale(sc + gi * 2, sdt));
+        for (int q = 0; q < 16; q++) lut[gi * 16 + (size_t)q] = (float)(q - 8) * s;
+    }
+    float acc = 0.0f;
+    for (size_t b = 0; b < pk; b++) {
+        size_t col = b * 2;
+        if (col >= k) break;
+        size_t gi = col / g;
+        if (gi > ng - 1) gi = ng - 1;
+        uint8_t p = rowp[b];
+        acc += x[col] * lut[gi * 16 + (p & 0x0f)];
+        if (col + 1 < k) acc += x[col + 1] * lut[gi * 16 + (p >> 4)];
+    }
+    return acc;
+}
+
+static void int4_rows(void *vctx, size_t r0, size_t r1)
+{
+    int4_ctx *c = (int4_ctx *)vctx;
+    size_t ng = (c->k + c->g - 1) / c->g;
+    float *lut = (float *)malloc(sizeof(float) * 16 * ng);
+    for (size_t r = r0; r < r1; r++) c->acc[r] = int4_row(c->x, c->page, c->k, c->m, c->g, c->sdt, r, lut);
+    free(lut);
+}
+
+void v3o_matmul_int4_acc(const float *x, const uint8_t *page, size_t k, size_t m, size_t g,
+                         int scale_dt, float *acc, int nthreads)
+{
+    int4_ctx c = {x, page, k, m, g, scale_dt, acc};
+    parallel_rows(m, nthreads, int4_rows, &c);
+}
+
+void v3o_partial_matmul_int4(const uint16_t *x_f16, const uint8_t *page, uint16_t *out_f16,
+                             size_t k, size_t m)
+{
+    float *x = (float *)malloc(sizeof(float) * k);
+    float *acc = (float *)malloc(sizeof(float) * m);
+    for (size_t i = 0; i < k; i++) x[i] = v3o_f16_to_f32(x_f16[i]);
+    v3o_matmul_int4_acc(x, page, k, m, 32, V3O_BF16, acc, 0);
+    for (size_t r = 0; r < m; r++) out_f16[r] = v3o_f32_to_f16(acc[r]);
+    free(x);
+    free(acc);
+}
+
+/* ------------------------------------------------------------------ INT4 SwiGLU */
+
+typedef struct {
+    const float *x;
+    const uint8_t *up, *gate;
+    size_t k, m, g;
+    int sdt;
+    float *h;
+} swiglu_ctx;
+
+static inline float silu_times(float gate, float up)
+{
+    /* kernels.rs:3041: silu = gate / (1 + (-gate).exp()); silu * up */
+    float silu = gate / (1.0f + expf(-gate));
+    return silu * up;
+}
+
+/* cpu_swiglu_int4 (kernels.rs:2959-3043): the two dot products interleave per byte, but each
+ * accumulator sees exactly the same sequence of rounded operations as a single-matrix row. */
+static void swiglu_rows(void *vctx, size_t r0, size_t r1)
+{
+    swiglu_ctx *c = (swiglu_ctx *)vctx;
+    size_t ng = (c->k + c->g - 1) / c->g;
+    float *lut = (float *)malloc(sizeof(float) * 16 * ng);
+    for (size_t r = r0; r < r1; r++) {
+        float up = int4_row(c->x, c->up, c->k, c->m, c->g, c->sdt, r, lut);
+        float gate = int4_row(c->x, c->gate, c->k, c->m, c->g, c->sdt, r, lut);
+        c->h[r] = silu_times(gate, up);
+    }
+    free(lut);
+}
+
+void v3o_swiglu_int4_acc(const float *x, const uint8_t *up_page, const uint8_t *gate_page,
+                         size_t k, size_t m, size_t g, int scale_dt, float *h, int nthreads)
+{
+    swiglu_ctx c = {x, up_page, gate_page, k, m, g, scale_dt, h};
+    parallel_rows(m, nthreads, swiglu_rows, &c);
+}
+
+void v3o_partial_swiglu_int4(const uint16_t *x_f16, const uint8_t *up_page,
+                             const uint8_t *gate_page, uint16_t *out_f16, size_t k, size_t m)
+{
+    float *x = (float *)malloc(sizeof(float) * k);
+    float *h = (float *)malloc(sizeof(float) * m);
+    for (size_t i = 0; i < k; i++) x[i] = v3o_f16_to_f32(x_f16[i]);
+    v3o_swiglu_int4_acc(x, up_page, gate_page, k, m, 32, V3O_BF16, h, 0);
+    for (size_t r = 0; r < m; r++) out_f16[r] = v3o_f32_to_f16(h[r]);
+    free(x);
+    free(h);
+}
+
+/* ------------------------------------------------------------------ accumulate */
+
+void v3o_weighted_accumulate_f32(float *out, const uint16_t *expert_f16, float w, size_t n)
+{
+    for (size_t i = 0; i < n; i++) out[i] += w * v3o_f16_to_f32(expert_f16[i]);
+}
+
+/* ------------------------------------------------------------------ router */
+
+typedef struct {
+    const float *x;
+    const void *w;
+    int wdt;
+    size_t d;
+    float *scores;
+} router_ctx;
+
+static void router_rows(void *vctx, size_t r0, size_t r1)
+{
+    router_ctx *c = (router_ctx *)vctx;
+    for (size_t e = r0; e < r1; e++) {
+        float acc = 0.0f;
+        if (c->wdt == V3O_F32) {
+            const float *row = (const float *)c->w + e * c->d;
+            for (size_t i = 0; i < c->d; i++) acc += c->x[i] * row[i];
+        } else {
+            const uint16_t *row = (const uint16_t *)c->w + e * c->d;
+            for (size_t i = 0; i < c->d; i++)
+                acc += c->x[i] * (c->wdt == V3O_F16 ? v3o_f16_to_f32(row[i]) : v3o_bf16_to_f32(row[i]));
+        }
+        c->scores[e] = acc;
+    }
+}
+
+/* Stable descending selection of the k largest keys: equal keys keep ascending index order,
+ * which is what Rust's stable `sort_by(|a, b| b.partial_cmp(a))` + truncate(k) yields for
+ * non-NaN keys (kernels.rs:2370-2371, :2416-2417). */
+static void stable_topk_desc(const float *key, size_t n, size_t k, size_t *idx_out)
+{
+    unsigned char *taken = (unsigned char *)calloc(n, 1);
+    for (size_t j = 0; j < k; j++) {
+        size_t best = (size_t)-1;
+        for (size_t i = 0; i < n; i++) {
+            if (taken[i]) continue;
+            if (best == (size_t)-1 || key[i] > key[best]) best = i;
+        }
+        taken[best] = 1;
+        idx_out[j] = best;
+    }
+    free(taken);
+}
+
+int v3o_router(const float *x, const void *w, int w_dt, size_t num_experts, size_t hidden,
+               size_t top_k, int mode, float scaling, int normalize, const float *bias,
+               uint16_t *ids, float *weights, float *scores_out, int nthreads)
+{
+    if (top_k == 0 || top_k > num_experts || num_experts > 65536) return -1;
+    float *scores = (float *)malloc(sizeof(float) * num_experts);
+    router_ctx c = {x, w, w_dt, hidden, scores};
+    parallel_rows(num_experts, nthreads, router_rows, &c);
+    if (scores_out) memcpy(scores_out, scores, sizeof(float) * num_experts);
+    size_t *sel = (size_t *)malloc(sizeof(size_t) * top_k);
+    if (mode == 0) {
+        /* kernels.rs:2368-2387 */
+        stable_topk_desc(scores, num_experts, top_k, sel);
+        float mx = -INFINITY;
+        for (size_t j = 0; j < top_k; j++) mx = fmaxf(mx, scores[sel[j]]);
+        float sum = 0.0f;
+        for (size_t j = 0; j < top_k; j++) sum += expf(scores[sel[j]] - mx);
+        for (size_t j = 0; j < top_k; j++) {
+            ids[j] = (uint16_t)sel[j];
+            weights[j] = expf(scores[sel[j]] - mx) / sum;
+        }
+    } else {
+        /* kernels.rs:2389-2436 */
+        float *sig = (float *)malloc(sizeof(float) * num_experts);
+        float *selk = (float *)malloc(sizeof(float) * num_experts);
+        for (size_t e = 0; e < num_experts; e++) {
+            sig[e] = 1.0f / (1.0f + expf(-scores[e]));
+            selk[e] = bias ? sig[e] + bias[e] : sig[e];
+        }
+        stable_topk_desc(selk, num_experts, top_k, sel);
+        for (size_t j = 0; j < top_k; j++) { ids[j] = (uint16_t)sel[j]; weights[j] = sig[sel[j]]; }
+        if (normalize) {
+            float total = 0.0f;
+            for (size_t j = 0; j < top_k; j++) total += weights[j];
+            if (total > 1e-20f)
+                for (size_t j = 0; j < top_k; j++) weights[j] /= total;
+        }
+        for (size_t j = 0; j < top_k; j++) weights[j] *= scaling;
+        free(sig);
+        free(selk);
+    }
+    free(sel);
+    free(scores);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ quantizer */
+
+/* quantize_weights_to_int4 (kernels.rs:3778-3831) with g as a parameter. Rust's f32::round is
+ * half-away-from-zero, which is C's roundf; `as i32` then clamp(0, 15). */
+void v3o_quantize_int4(const float *w, size_t rows, size_t cols, size_t g, uint8_t *out)
+{
+    size_t pk = (cols + 1) / 2, ng = (cols + g - 1) / g;
+    memset(out, 0, rows * pk + rows * ng * 2);
+    uint8_t *sc = out + rows * pk;
+    for (size_t r = 0; r < rows; r++) {
+        const float *row = w + r * cols;
+        for (size_t gi = 0; gi < ng; gi++) {
+            size_t c0 = gi * g, c1 = c0 + g < cols ? c0 + g : cols;
+            float mx = 0.0f;
+            for (size_t c = c0; c < c1; c++) mx = fmaxf(mx, fabsf(row[c]));
+            float scale = mx > 0.0f ? mx / 7.0f : 1.0f;
+            uint16_t sb = v3o_f32_to_bf16(scale);
+            sc[(r * ng + gi) * 2] = (uint8_t)(sb & 0xff);
+            sc[(r * ng + gi) * 2 + 1] = (uint8_t)(sb >> 8);
+            for (size_t c = c0; c < c1; c++) {
+                int q = (int)roundf(row[c] / scale) + 8;
+                q = q < 0 ? 0 : (q > 15 ? 15 : q);
+                if (c % 2 == 0) out[r * pk + c / 2] |= (uint8_t)(q & 0x0f);
+                else out[r * pk + c / 2] |= (uint8_t)((q & 0x0f) << 4);
+            }
+        }
+    }
+}
+
+/* dequantize_int4_to_f32 (kernels.rs:3866-3927): (q - 8) * scale, scale in dt. */
+void v3o_dequantize_int4(const uint8_t *page, size_t rows, size_t cols, size_t g, int scale_dt,
+                         float *out)
+{
+    size_t pk = (cols + 1) / 2, ng = (cols + g - 1) / g;
+    const uint8_t *sc = page + rows * pk;
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < cols; c++) {
+            uint8_t b = page[r * pk + c / 2];
+            int q = (c % 2 == 0) ? (b & 0x0f) : (b >> 4);
+            float s = decode_scale(sc + (r * ng + c / g) * 2, scale_dt);
+            out[r * cols + c] = (float)(q - 8) * s;
+        }
+}
+
+/* ------------------------------------------------------------------ MoE layer */
+
+/* execute_expert (engine.rs:5801-6306) for INT4 pages: up/gate pages are paired in order and
+ * each pair writes rows [p*R, p*R + rows) of h; each down page reads the whole h. */
+static void run_expert(const float *x, size_t hidden, size_t inter, size_t g, int sdt,
+                       const v3o_expert *ex, float weight, int faithful, float *out, int nthreads)
+{
+    float *h = (float *)calloc(inter, sizeof(float));
+    float *tmp = (float *)malloc(sizeof(float) * (inter > hidden ? inter : hidden));
+    for (size_t p = 0; p < ex->up.npages && p < ex->gate.npages; p++) {
+        size_t r0 = p * ex->up.rows_per_page;
+        size_t rows = inter - r0 < ex->up.rows_per_page ? inter - r0 : ex->up.rows_per_page;
+        v3o_swiglu_int4_acc(x, ex->up.pages[p], ex->gate.pages[p], hidden, rows, g, sdt, tmp,
+                            nthreads);
+        for (size_t r = 0; r < rows; r++)
+            h[r0 + r] = faithful ? v3o_f16_to_f32(v3o_f32_to_f16(tmp[r])) : tmp[r];
+    }
+    for (size_t p = 0; p < ex->down.npages; p++) {
+        size_t r0 = p * ex->down.rows_per_page;
+        size_t rows = hidden - r0 < ex->down.rows_per_page ? hidden - r0 : ex->down.rows_per_page;
+        v3o_matmul_int4_acc(h, ex->down.pages[p], inter, rows, g, sdt, tmp, nthreads);
+        for (size_t r = 0; r < rows; r++) {
+            float d = faithful ? v3o_f16_to_f32(v3o_f32_to_f16(tmp[r])) : tmp[r];
+            out[r0 + r] += weight * d; /* weighted_accumulate_f32, kernels.rs:2033 */
+        }
+    }
+    free(h);
+    free(tmp);
+}
+
+void v3o_moe_layer(const float *x, size_t hidden, size_t inter, size_t g, int scale_dt,
+                   const v3o_expert *routed, const uint16_t *ids, const float *weights,
+                   size_t top_k, const v3o_expert *shared, size_t n_shared, int faithful,
+                   float *out, int nthreads)
+{
+    memset(out, 0, sizeof(float) * hidden); /* layer_output_buf.zero_async, engine.rs:5200 */
+    for (size_t j = 0; j < top_k; j++)
+        run_expert(x, hidden, inter, g, scale_dt, &routed[ids[j]], weights[j], faithful, out, nthreads);
+    for (size_t s = 0; s < n_shared; s++)
+        run_expert(x, hidden, inter, g, scale_dt, &shared[s], 1.0f, faithful, out, nthreads);
+}
+
+/* ------------------------------------------------------------------ MXFP4 */
+
+/* kernels.cu:438-441: bit3 sign, bits2-1 exponent, bit0 mantissa. */
+float v3o_e2m1(uint8_t code)
+{
+    static const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+    float v = mag[code & 7];
+    return (code & 8) ? -v : v;
+}
+
+/* kernels.cu:2770-2777: the E8M0 byte is placed in the f32 exponent field: 2^(e-127), e=0 -> 0. */
+float v3o_e8m0(uint8_t e) { return u2f((uint32_t)e << 23); }
+
+typedef struct {
+    const float *x;
+    const uint8_t *codes, *scales;
+    size_t k, m;
+    float *acc;
+} mx_ctx;
+
+static void mx_rows(void *vctx, size_t r0, size_t r1)
+{
+    mx_ctx *c = (mx_ctx *)vctx;
+    size_t pk = (c->k + 1) / 2, nb = (c->k + 31) / 32;
+    for (size_t r = r0; r < r1; r++) {
+        float acc = 0.0f;
+        for (size_t col = 0; col < c->k; col++) {
+            uint8_t b = c->codes[r * pk + col / 2];
+            uint8_t q = (col % 2 == 0) ? (b & 0x0f) : (b >> 4);
+            float wv = v3o_e2m1(q) * v3o_e8m0(c->scales[r * nb + col / 32]);
+            acc += c->x[col] * wv;
+        }
+        c->acc[r] = acc;
+    }
+}
+
+void v3o_matmul_mxfp4_acc(const float *x, const uint8_t *codes, const uint8_t *scales, size_t k,
+                          size_t m, float *acc, int nthreads)
+{
+    mx_ctx c = {x, codes, scales, k, m, acc};
+    parallel_rows(m, nthreads, mx_rows, &c);
+}
+
+/* ------------------------------------------------------------------ synthetic data */
+
+static inline uint64_t mix64(uint64_t z)
+{
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+uint64_t v3o_synth_hash(uint64_t seed, uint64_t stream, uint64_t ctr)
+{
+    uint64_t z = seed ^ (stream * 0xD1B54A32D192ED03ull);
+    z += (ctr + 1ull) * 0x9E3779B97F4A7C15ull;
+    z = mix64(z);
+    return mix64(z + 0x9E3779B97F4A7C15ull);
+}
+
+/* Irwin-Hall(4) of 16-bit uniforms, centred and scaled to unit variance:
+ * (sum - 131070) / 37837.23 with the constant rounded to f32 (2.6429e-5f). Integer sum is
+ * exact; the single f32 multiply is the only rounding, so host and device agree bit for bit. */
+float v3o_synth_normal(uint64_t seed, uint64_t stream, uint64_t ctr)
+{
+    uint64_t h = v3o_synth_hash(seed, stream, ctr);
+    int32_t s = (int32_t)(h & 0xffff) + (int32_t)((h >> 16) & 0xffff) +
+                (int32_t)((h >> 32) & 0xffff) + (int32_t)(h >> 48) - 131070;
+    return (float)s * 2.6429e-5f;
+}
+
+void v3o_synth_bytes(uint64_t seed, uint64_t stream, size_t off, size_t n, uint8_t *dst)
+{
+    for (size_t i = 0; i < n; i++) {
+        size_t j = off + i;
+        dst[i] = (uint8_t)(v3o_synth_hash(seed, stream, j >> 3) >> (8 * (j & 7)));
+    }
+}
+
+static uint16_t round_to(float v, int dt)
+{
+    return dt == V3O_F16 ? v3o_f32_to_f16(v) : v3o_f32_to_bf16(v);
+}
+
+uint16_t v3o_synth_scale(uint64_t seed, uint64_t stream, uint64_t idx, float sigma, int dt)
+{
+    for (uint64_t t = 0;; t++) {
+        float v = fabsf(v3o_synth_normal(seed, stream, idx + (t << 40))) * sigma;
+        uint16_t b = round_to(v, dt);
+        if ((b & 0x7fff) != 0) return b;
+    }
+}
+
+void v3o_synth_normal_array(uint64_t seed, uint64_t stream, size_t off, size_t n, float sigma,
+                            int dt, void *dst)
+{
+    for (size_t i = 0; i < n; i++) {
+        float v = v3o_synth_normal(seed, stream, off + i) * sigma;
+        if (dt == V3O_F32) ((float *)dst)[i] = v;
+        else ((uint16_t *)dst)[i] = round_to(v, dt);
+    }
+}
+
+void v3o_synth_int4_page(uint64_t seed, uint64_t stream, size_t k, size_t g, int scale_dt,
+                         float sigma, size_t row_start, size_t rows, uint8_t *page)
+{
+    size_t pk = (k + 1) / 2, ng = (k + g - 1) / g;
+    v3o_synth_bytes(seed, stream * 2, row_start * pk, rows * pk, page);
+    uint8_t *sc = page + rows * pk;
+    for (size_t i = 0; i < rows * ng; i++) {
+        uint16_t b = v3o_synth_scale(seed, stream * 2 + 1, row_start * ng + i, sigma, scale_dt);
+        sc[2 * i] = (uint8_t)(b & 0xff);
+        sc[2 * i + 1] = (uint8_t)(b >> 8);
+    }
+}

@@ -1,0 +1,139 @@
+/*
+ * oracle/cpu_ref.h — CPU restatement of vib3's MoE expert path (TEST INFRASTRUCTURE ONLY).
+ *
+ * This library is the parity oracle for the HIP kernels in vib3_amd/csrc. It restates, in plain
+ * C with sequential fp32 arithmetic (built with -ffp-contract=off so a*b+c is never fused), the
+ * CPU fallback of the reference crate (threehundobaud/vic, crate `vib3`):
+ *
+ *   v3o_matmul_int4_acc      <- src/compute/kernels.rs:2746-2832 (cpu_matmul_int4_grouped)
+ *   v3o_partial_matmul_int4  <- src/compute/kernels.rs:25-67, :2733 (partial_matmul, INT4 arm)
+ *   v3o_swiglu_int4_acc      <- src/compute/kernels.rs:2932-3054 (cpu_swiglu_int4)
+ *   v3o_partial_swiglu_int4  <- src/compute/kernels.rs:162-203 (partial_swiglu, INT4 arm)
+ *   v3o_weighted_accumulate_f32 <- src/compute/kernels.rs:2000-2036
+ *   v3o_router               <- src/compute/kernels.rs:2307-2440 (run_router_with_scoring_and_bias)
+ *   v3o_quantize_int4        <- src/compute/kernels.rs:3778-3831 (quantize_weights_to_int4)
+ *   v3o_dequantize_int4      <- src/compute/kernels.rs:3866-3927 (dequantize_int4_to_f32)
+ *   v3o_moe_layer            <- src/runtime/engine.rs:5801-6306 (execute_expert),
+ *                               :6317-6456 (execute_shared_expert, weight 1.0 without gate)
+ *   v3o_mxfp4_*              <- cuda/src/kernels.cu:438-441 (E2M1 table), :2770-2777 (E8M0)
+ *   v3o_synth_*              synthetic-data generator spec shared with vib3_amd/csrc/synth.hip
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library,
+ * and only as the checker / the timed CPU baseline. The product path never calls it.
+ *
+ * Parity pins (what checks each function independently of its own formula) are listed in
+ * tests/test_oracle.py: the reference's known-answer tests, f64 brute force on small shapes,
+ * closed forms and invariants. Functions whose rounding points only a restatement can fix
+ * (sequential fp32 sum order, f16 output rounding, libm expf) are pinned up to those points.
+ */
+#ifndef VIB3_ORACLE_CPU_REF_H
+#define VIB3_ORACLE_CPU_REF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes shared with include/vib3_hip.h */
+enum { V3O_F32 = 0, V3O_F16 = 1, V3O_BF16 = 2 };
+
+/* IEEE conversions with round-to-nearest-even, the semantics of `half` 2.7.1
+ * (Cargo.lock:885-886) used by the reference for f16/bf16 <-> f32. */
+uint16_t v3o_f32_to_f16(float f);
+float v3o_f16_to_f32(uint16_t h);
+uint16_t v3o_f32_to_bf16(float f);
+float v3o_bf16_to_f32(uint16_t b);
+/* convert n elements of dtype `dt` at src to f32 */
+void v3o_to_f32(const void *src, int dt, size_t n, float *dst);
+
+/* Number of worker threads used by the row-parallel functions when nthreads <= 0. */
+int v3o_default_threads(void);
+
+/* INT4 page: [m x ceil(k/2)] packed nibbles (low nibble = even column, stored q = code+8),
+ * then [m x ceil(k/g)] little-endian 2-byte scales (scale_dt = V3O_BF16 or V3O_F16).
+ * acc[row] = sum_k x[k] * LUT_g[q]  with LUT_g[q] = (q-8)*s_g  (sequential fp32, k order).
+ * Invalid scale (non-finite or <= 0) decodes as 1/8 (kernels.rs:2791-2797). */
+void v3o_matmul_int4_acc(const float *x, const uint8_t *page, size_t k, size_t m, size_t g,
+                         int scale_dt, float *acc, int nthreads);
+
+/* Public CPU entry of partial_matmul(..., DType::INT4): f16 in, f16 out, g = 32, BF16 scales. */
+void v3o_partial_matmul_int4(const uint16_t *x_f16, const uint8_t *page, uint16_t *out_f16,
+                             size_t k, size_t m);
+
+/* h[row] = silu(gate_acc) * up_acc (fp32, before the f16 rounding of the reference). */
+void v3o_swiglu_int4_acc(const float *x, const uint8_t *up_page, const uint8_t *gate_page,
+                         size_t k, size_t m, size_t g, int scale_dt, float *h, int nthreads);
+
+/* Public CPU entry of partial_swiglu(..., DType::INT4): f16 in/out, g = 32, BF16 scales. */
+void v3o_partial_swiglu_int4(const uint16_t *x_f16, const uint8_t *up_page,
+                             const uint8_t *gate_page, uint16_t *out_f16, size_t k, size_t m);
+
+/* out[i] += w * f32(expert_f16[i]) */
+void v3o_weighted_accumulate_f32(float *out, const uint16_t *expert_f16, float w, size_t n);
+
+/* Router: scores[e] = sum_d x[d]*W[e][d] (sequential fp32), then
+ * mode 0 (softmax): stable sort desc on scores, keep k, softmax over the k;
+ * mode 1 (sigmoid): sel = sigmoid + bias, stable sort desc, keep k, weight = sigmoid,
+ *                   normalise if sum > 1e-20 and `normalize`, then * scaling.
+ * W dtype: V3O_F32 / V3O_F16 / V3O_BF16. bias may be NULL. scores_out may be NULL.
+ * Returns 0, or -1 for bad arguments. */
+int v3o_router(const float *x, const void *w, int w_dt, size_t num_experts, size_t hidden,
+               size_t top_k, int mode, float scaling, int normalize, const float *bias,
+               uint16_t *ids, float *weights, float *scores_out, int nthreads);
+
+/* Quantizer with the group size as a parameter (the reference fixes g = 32). Scales BF16. */
+void v3o_quantize_int4(const float *w, size_t rows, size_t cols, size_t g, uint8_t *out);
+void v3o_dequantize_int4(const uint8_t *page, size_t rows, size_t cols, size_t g, int scale_dt,
+                         float *out);
+
+/* One expert's matrices: each is a list of pages with a uniform row count per page
+ * (the last page may be shorter); each page holds [rows x pk][rows x G x 2] like a
+ * vib3 INT4 page (kernels.rs:95-98, convert.rs:1807-1880). */
+typedef struct {
+    const uint8_t *const *pages; /* npages pointers */
+    size_t npages;
+    size_t rows_per_page;
+} v3o_matrix;
+
+typedef struct {
+    v3o_matrix up, gate, down; /* segment 0 = up, 1 = gate, 2 = down (types.rs:200) */
+} v3o_expert;
+
+/* MoE layer as the engine composes it: for each selected expert (router order):
+ *   h = f16(silu(gate.x) * up.x)  per up/gate page pair into h[row_start..]
+ *   d = f16(down . h)             per down page
+ *   out += w * d                  (weighted_accumulate_f32)
+ * then each shared expert with weight 1.0. out is zeroed first.
+ * faithful = 1 keeps the reference's f16 rounding of h and d; 0 keeps them fp32. */
+void v3o_moe_layer(const float *x, size_t hidden, size_t inter, size_t g, int scale_dt,
+                   const v3o_expert *routed, const uint16_t *ids, const float *weights,
+                   size_t top_k, const v3o_expert *shared, size_t n_shared, int faithful,
+                   float *out, int nthreads);
+
+/* MXFP4: E2M1 code (low nibble = even k) times E8M0 scale 2^(e-127) per 32 along k. */
+float v3o_e2m1(uint8_t code);
+float v3o_e8m0(uint8_t e);
+/* acc[row] = sum_k x[k] * e2m1(q) * 2^(e-127)  (sequential fp32 over k; each term rounded) */
+void v3o_matmul_mxfp4_acc(const float *x, const uint8_t *codes, const uint8_t *scales, size_t k,
+                          size_t m, float *acc, int nthreads);
+
+/* ---- synthetic data generator (counter-based, identical spec in csrc/synth.hip) ---- */
+uint64_t v3o_synth_hash(uint64_t seed, uint64_t stream, uint64_t ctr);
+float v3o_synth_normal(uint64_t seed, uint64_t stream, uint64_t ctr);
+/* n bytes of uniform bits: byte j = (hash(seed, stream, j/8) >> 8*(j%8)) & 0xff */
+void v3o_synth_bytes(uint64_t seed, uint64_t stream, size_t off, size_t n, uint8_t *dst);
+/* rounded |N(0,1)|*sigma in dt (bf16/f16), redrawn while it rounds to zero */
+uint16_t v3o_synth_scale(uint64_t seed, uint64_t stream, uint64_t idx, float sigma, int dt);
+/* normal(0,1)*sigma written as dt (f32/f16/bf16) for indices [off, off+n) */
+void v3o_synth_normal_array(uint64_t seed, uint64_t stream, size_t off, size_t n, float sigma,
+                            int dt, void *dst);
+/* Write rows [row_start, row_start+rows) of the logical INT4 matrix (stream, k, g) as one page. */
+void v3o_synth_int4_page(uint64_t seed, uint64_t stream, size_t k, size_t g, int scale_dt,
+                         float sigma, size_t row_start, size_t rows, uint8_t *page);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

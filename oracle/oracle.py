@@ -1,0 +1,259 @@
+"""ctypes front end of the CPU oracle (oracle/cpu_ref.c). TEST INFRASTRUCTURE ONLY.
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg import this
+module, and only to check or to time the reference algorithm. Each function names the
+reference code it restates (threehundobaud/vic, crate ``vib3``).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+F32, F16, BF16 = 0, 1, 2
+_lib = None
+
+
+def build() -> None:
+    """Compile liboracle.so from cpu_ref.c (gcc, -ffp-contract=off)."""
+    subprocess.check_call(["make", "-s", "-B", "-C", _HERE, "liboracle.so"])
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = C.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L: C.CDLL) -> None:
+    P, S, I, F, U64 = C.c_void_p, C.c_size_t, C.c_int, C.c_float, C.c_uint64
+    sig = {
+        "v3o_f32_to_f16": (C.c_uint16, [F]),
+        "v3o_f16_to_f32": (F, [C.c_uint16]),
+        "v3o_f32_to_bf16": (C.c_uint16, [F]),
+        "v3o_bf16_to_f32": (F, [C.c_uint16]),
+        "v3o_default_threads": (I, []),
+        "v3o_matmul_int4_acc": (None, [P, P, S, S, S, I, P, I]),
+        "v3o_partial_matmul_int4": (None, [P, P, P, S, S]),
+        "v3o_swiglu_int4_acc": (None, [P, P, P, S, S, S, I, P, I]),
+        "v3o_partial_swiglu_int4": (None, [P, P, P, P, S, S]),
+        "v3o_weighted_accumulate_f32": (None, [P, P, F, S]),
+        "v3o_router": (I, [P, P, I, S, S, S, I, F, I, P, P, P, P, I]),
+        "v3o_quantize_int4": (None, [P, S, S, S, P]),
+        "v3o_dequantize_int4": (None, [P, S, S, S, I, P]),
+        "v3o_moe_layer": (None, [P, S, S, S, I, P, P, P, S, P, S, I, P, I]),
+        "v3o_e2m1": (F, [C.c_uint8]),
+        "v3o_e8m0": (F, [C.c_uint8]),
+        "v3o_matmul_mxfp4_acc": (None, [P, P, P, S, S, P, I]),
+        "v3o_synth_hash": (U64, [U64, U64, U64]),
+        "v3o_synth_normal": (F, [U64, U64, U64]),
+        "v3o_synth_bytes": (None, [U64, U64, S, S, P]),
+        "v3o_synth_scale": (C.c_uint16, [U64, U64, U64, F, I]),
+        "v3o_synth_normal_array": (None, [U64, U64, S, S, F, I, P]),
+        "v3o_synth_int4_page": (None, [U64, U64, S, S, I, F, S, S, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------- conversions
+
+def f16_bits(x) -> np.ndarray:
+    """f32 -> f16 bit patterns (RNE), via the oracle's own converter."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    fn = lib().v3o_f32_to_f16
+    return np.array([fn(float(v)) for v in x], dtype=np.uint16)
+
+
+def to_f32(bits: np.ndarray, dt: int) -> np.ndarray:
+    bits = np.ascontiguousarray(bits)
+    if dt == F32:
+        return bits.astype(np.float32)
+    if dt == BF16:
+        return (bits.astype(np.uint32) << 16).view(np.float32)
+    return bits.view(np.float16).astype(np.float32)
+
+
+# ---------------------------------------------------------------- kernels
+
+def matmul_int4_acc(x: np.ndarray, page: np.ndarray, k: int, m: int, g: int, scale_dt: int,
+                    nthreads: int = 0) -> np.ndarray:
+    """kernels.rs:2746 cpu_matmul_int4_grouped, fp32 accumulators before f16 rounding."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    page = np.ascontiguousarray(page, dtype=np.uint8)
+    out = np.empty(m, dtype=np.float32)
+    lib().v3o_matmul_int4_acc(_p(x), _p(page), k, m, g, scale_dt, _p(out), nthreads)
+    return out
+
+
+def partial_matmul_int4(x_f16: np.ndarray, page: np.ndarray, k: int, m: int) -> np.ndarray:
+    """kernels.rs:25 partial_matmul(DType::INT4) CPU branch: f16 bits in and out."""
+    x_f16 = np.ascontiguousarray(x_f16, dtype=np.uint16)
+    page = np.ascontiguousarray(page, dtype=np.uint8)
+    out = np.empty(m, dtype=np.uint16)
+    lib().v3o_partial_matmul_int4(_p(x_f16), _p(page), _p(out), k, m)
+    return out
+
+
+def swiglu_int4_acc(x, up_page, gate_page, k, m, g, scale_dt, nthreads=0) -> np.ndarray:
+    """kernels.rs:2932 cpu_swiglu_int4, silu(gate)*up in fp32 before f16 rounding."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    up_page = np.ascontiguousarray(up_page, dtype=np.uint8)
+    gate_page = np.ascontiguousarray(gate_page, dtype=np.uint8)
+    out = np.empty(m, dtype=np.float32)
+    lib().v3o_swiglu_int4_acc(_p(x), _p(up_page), _p(gate_page), k, m, g, scale_dt, _p(out), nthreads)
+    return out
+
+
+def partial_swiglu_int4(x_f16, up_page, gate_page, k, m) -> np.ndarray:
+    """kernels.rs:162 partial_swiglu(DType::INT4) CPU branch: f16 bits in and out."""
+    x_f16 = np.ascontiguousarray(x_f16, dtype=np.uint16)
+    up_page = np.ascontiguousarray(up_page, dtype=np.uint8)
+    gate_page = np.ascontiguousarray(gate_page, dtype=np.uint8)
+    out = np.empty(m, dtype=np.uint16)
+    lib().v3o_partial_swiglu_int4(_p(x_f16), _p(up_page), _p(gate_page), _p(out), k, m)
+    return out
+
+
+def weighted_accumulate_f32(out: np.ndarray, expert_f16: np.ndarray, w: float) -> None:
+    """kernels.rs:2000 weighted_accumulate_f32 CPU branch (in place)."""
+    assert out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
+    e = np.ascontiguousarray(expert_f16, dtype=np.uint16)
+    lib().v3o_weighted_accumulate_f32(_p(out), _p(e), float(w), out.size)
+
+
+def router(x, w, w_dt, num_experts, hidden, top_k, mode, scaling=1.0, normalize=True,
+           bias=None, nthreads=0):
+    """kernels.rs:2307 run_router_with_scoring_and_bias CPU branch.
+
+    Returns (ids uint16[k], weights f32[k], scores f32[E])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w)
+    ids = np.empty(top_k, dtype=np.uint16)
+    wts = np.empty(top_k, dtype=np.float32)
+    scores = np.empty(num_experts, dtype=np.float32)
+    b = None
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, dtype=np.float32)
+        b = _p(bias)
+    rc = lib().v3o_router(_p(x), _p(w), w_dt, num_experts, hidden, top_k, mode, float(scaling),
+                          int(bool(normalize)), b, _p(ids), _p(wts), _p(scores), nthreads)
+    if rc != 0:
+        raise ValueError("oracle router: bad arguments")
+    return ids, wts, scores
+
+
+def quantize_int4(w: np.ndarray, rows: int, cols: int, g: int = 32) -> np.ndarray:
+    """kernels.rs:3778 quantize_weights_to_int4 (g generalised)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    pk, ng = (cols + 1) // 2, (cols + g - 1) // g
+    out = np.zeros(rows * pk + rows * ng * 2, dtype=np.uint8)
+    lib().v3o_quantize_int4(_p(w), rows, cols, g, _p(out))
+    return out
+
+
+def dequantize_int4(page, rows, cols, g, scale_dt) -> np.ndarray:
+    """kernels.rs:3866 dequantize_int4_to_f32."""
+    page = np.ascontiguousarray(page, dtype=np.uint8)
+    out = np.empty(rows * cols, dtype=np.float32)
+    lib().v3o_dequantize_int4(_p(page), rows, cols, g, scale_dt, _p(out))
+    return out.reshape(rows, cols)
+
+
+class _Matrix(C.Structure):
+    _fields_ = [("pages", C.POINTER(C.c_void_p)), ("npages", C.c_size_t),
+                ("rows_per_page", C.c_size_t)]
+
+
+class _Expert(C.Structure):
+    _fields_ = [("up", _Matrix), ("gate", _Matrix), ("down", _Matrix)]
+
+
+def _expert_struct(pages_by_seg, rows_by_seg, keep):
+    """pages_by_seg: 3 lists of uint8 page arrays (up, gate, down)."""
+    ex = _Expert()
+    for name, pages, rpp in zip(("up", "gate", "down"), pages_by_seg, rows_by_seg):
+        arr = (C.c_void_p * len(pages))(*[p.ctypes.data for p in pages])
+        keep.append(arr)
+        keep.extend(pages)
+        setattr(ex, name, _Matrix(C.cast(arr, C.POINTER(C.c_void_p)), len(pages), rpp))
+    return ex
+
+
+def moe_layer(x, hidden, inter, g, scale_dt, routed, ids, weights, shared, faithful=True,
+              nthreads=0) -> np.ndarray:
+    """engine.rs:5801 execute_expert x k + :6317 execute_shared_expert, summed in f32.
+
+    routed: dict expert_id -> (pages_by_seg, rows_by_seg); only ids need to be present.
+    shared: list of (pages_by_seg, rows_by_seg)."""
+    keep = []
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ids = np.ascontiguousarray(ids, dtype=np.uint16)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    n_routed = int(ids.max()) + 1 if ids.size else 0
+    arr = (_Expert * max(n_routed, 1))()
+    for e in set(int(i) for i in ids):
+        pages, rows = routed[e]
+        arr[e] = _expert_struct(pages, rows, keep)
+    sh = (_Expert * max(len(shared), 1))()
+    for s, (pages, rows) in enumerate(shared):
+        sh[s] = _expert_struct(pages, rows, keep)
+    out = np.empty(hidden, dtype=np.float32)
+    lib().v3o_moe_layer(_p(x), hidden, inter, g, scale_dt, C.cast(arr, C.c_void_p), _p(ids),
+                        _p(weights), ids.size, C.cast(sh, C.c_void_p), len(shared),
+                        int(bool(faithful)), _p(out), nthreads)
+    return out
+
+
+def e2m1(code: int) -> float:
+    return lib().v3o_e2m1(code)
+
+
+def e8m0(e: int) -> float:
+    return lib().v3o_e8m0(e)
+
+
+def matmul_mxfp4_acc(x, codes, scales, k, m, nthreads=0) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.uint8)
+    out = np.empty(m, dtype=np.float32)
+    lib().v3o_matmul_mxfp4_acc(_p(x), _p(codes), _p(scales), k, m, _p(out), nthreads)
+    return out
+
+
+# ---------------------------------------------------------------- synthetic data
+
+def synth_bytes(seed, stream, off, n) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint8)
+    lib().v3o_synth_bytes(seed, stream, off, n, _p(out))
+    return out
+
+
+def synth_normal_array(seed, stream, off, n, sigma, dt) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32 if dt == F32 else np.uint16)
+    lib().v3o_synth_normal_array(seed, stream, off, n, float(sigma), dt, _p(out))
+    return out
+
+
+def synth_int4_page(seed, stream, k, g, scale_dt, sigma, row_start, rows) -> np.ndarray:
+    pk, ng = (k + 1) // 2, (k + g - 1) // g
+    out = np.empty(rows * pk + rows * ng * 2, dtype=np.uint8)
+    lib().v3o_synth_int4_page(seed, stream, k, g, scale_dt, float(sigma), row_start, rows, _p(out))
+    return out
