@@ -1,0 +1,204 @@
+/*
+ * vib3_hip.h — C ABI of the MI355X (gfx950) MoE expert compute library, libvib3_hip.so.
+ *
+ * Drop-in for the MoE/router part of vib3's `extern "C"` launcher interface
+ * (threehundobaud/vic: src/compute/cuda_ffi.rs:143-1063, implemented there by
+ * cuda/src/kernels.cu). Conventions kept from the reference:
+ *   - every launcher is asynchronous on `stream` (a hipStream_t; NULL = the null stream);
+ *   - the return value is 0 on success, a positive hipError_t on a HIP error, and negative for
+ *     argument errors (-1 unsupported shape/dtype, -2 bad count, as kernels.cu:5671-5672;
+ *     -3 bad pointer/alignment, -4 workspace too small);
+ *   - all buffers are caller-owned device pointers; nothing here allocates device memory;
+ *   - INT4 pages are laid out as [m x ceil(k/2)] packed nibbles (low nibble = even column,
+ *     stored q = code + 8) followed by [m x ceil(k/g)] little-endian 2-byte scales
+ *     (kernels.rs:95-98, :3752-3825); dequantised weight = (q - 8) * scale.
+ *     A scale that is not finite or not > 0 decodes as 1/8, as the CPU fallback does
+ *     (kernels.rs:2791-2797).
+ *
+ * Fast paths need k % 32 == 0 and 16-byte aligned rows (k/2 % 16 == 0, page bases 16-byte
+ * aligned); other shapes run a simple HIP kernel with the same results. Activations given as
+ * f32 or bf16 must satisfy |x| < 65504 (the reference CPU path holds them in f16).
+ */
+#ifndef VIB3_HIP_H
+#define VIB3_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+#define VIB3_DT_F32 0
+#define VIB3_DT_F16 1
+#define VIB3_DT_BF16 2
+
+/* router scoring modes (kernels.rs:2226 RouterScoringFunc) */
+#define VIB3_ROUTER_SOFTMAX 0
+#define VIB3_ROUTER_SIGMOID 1
+
+/* error codes besides hipError_t */
+#define VIB3_ERR_UNSUPPORTED (-1)
+#define VIB3_ERR_BAD_COUNT (-2)
+#define VIB3_ERR_BAD_POINTER (-3)
+#define VIB3_ERR_WORKSPACE (-4)
+
+/* ------------------------------------------------------------------------------------------
+ * Reference-compatible launchers: same names, argument order and meaning as cuda_ffi.rs.
+ * ---------------------------------------------------------------------------------------- */
+
+/* cuda_ffi.rs:165 (kernels.cu:111, :1043): out_f16[m] = sum_k x_f16[k]*(q-8)*scale_f16.
+ * The reference GPU kernel decodes these scales as FP16 (kernels.cu:45, :140). */
+int vib3_launch_partial_matmul_int4(const void *input, const void *weight_packed,
+                                    const void *scales, void *output, int k, int m_slice,
+                                    int group_size, void *stream);
+
+/* cuda_ffi.rs:312 (kernels.cu:175, :1202): same with an f32 input vector. */
+int vib3_launch_partial_matmul_int4_f32(const void *input, const void *weight,
+                                        const void *scales, void *output, int k, int m_slice,
+                                        int group_size, void *stream);
+
+/* cuda_ffi.rs:344 (kernels.cu:279, :1278): out_f16[m] = silu(gate.x) * (up.x), f32 input,
+ * FP16 scales. One launch; the two GEMVs and SwiGLU are fused. */
+int vib3_launch_fused_swiglu_int4_f32(const void *input, const void *up_weight,
+                                      const void *up_scales, const void *gate_weight,
+                                      const void *gate_scales, void *output, int k, int m_slice,
+                                      int group_size, void *stream);
+
+/* cuda_ffi.rs:186 (kernels.cu:772): out_f16[i] = silu(a[i]) * b[i] for f16 a, b. Argument
+ * names follow the reference declaration; the Rust caller passes the gate result first
+ * (kernels.rs:283). */
+int vib3_launch_silu_mul(const void *up_result, const void *gate_result, void *output, int dim,
+                         void *stream);
+
+/* cuda_ffi.rs:202 (kernels.cu:803): out_f32[i] += weight * f32(expert_f16[i]). */
+int vib3_launch_weighted_accumulate_f32(void *output, const void *expert_output, float weight,
+                                        int dim, void *stream);
+
+/* cuda_ffi.rs:212 (kernels.cu:2092): out_f32[i] += weight * expert_f32[i]. */
+int vib3_launch_weighted_accumulate_f32_f32(void *output, const void *expert_output,
+                                            float weight, int dim, void *stream);
+
+/* cuda_ffi.rs:369 (kernels.cu:665, :1477): scores[e] = sum_d h_f32[d] * W_f16[e][d]. */
+int vib3_launch_router_gemv_f32(const void *hidden_state, const void *router_weights,
+                                float *scores, int hidden_dim, int num_experts, void *stream);
+
+/* cuda_ffi.rs:379 (kernels.cu:4075): router GEMV (f32 h, f16 W) + scoring + top-k on device,
+ * two launches like the reference. scoring_mode 0: softmax over the top-k of the raw scores;
+ * 1: sigmoid (+bias for selection only), normalised, times scaling_factor. Works for any
+ * num_experts <= 4096 (the reference kernel needs a power of two). */
+int vib3_launch_router_topk(const void *hidden_state, const void *router_weights,
+                            float *scores_buf, const float *bias, uint16_t *out_ids,
+                            float *out_weights, int hidden_dim, int num_experts, int top_k,
+                            int scoring_mode, float scaling_factor, void *stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Additive launchers (no counterpart in cuda_ffi.rs): explicit dtypes, page layout, group
+ * size and scale dtype, so one library serves the CPU-fallback semantics (BF16 scales,
+ * kernels.rs:2789) and the reference GPU semantics (FP16 scales, kernels.cu:45).
+ * ---------------------------------------------------------------------------------------- */
+
+/* partial_matmul (kernels.rs:25) on one INT4 page: output[m] = page . input.
+ * input_dtype: F32/F16/BF16; output_dtype: F32/F16; scale_dtype: F16/BF16. */
+int vib3_launch_partial_matmul_int4_ex(const void *input, int input_dtype,
+                                       const void *weight_page, void *output, int output_dtype,
+                                       int k, int m_slice, int group_size, int scale_dtype,
+                                       void *stream);
+
+/* partial_swiglu (kernels.rs:162) on one up page and one gate page, fused in one launch:
+ * output[m] = silu(gate . input) * (up . input). */
+int vib3_launch_partial_swiglu_int4_ex(const void *input, int input_dtype, const void *up_page,
+                                       const void *gate_page, void *output, int output_dtype,
+                                       int k, int m_slice, int group_size, int scale_dtype,
+                                       void *stream);
+
+/* run_router_with_scoring_and_bias (kernels.rs:2307) on device in one launch: logits with
+ * hidden/weight dtypes of choice, optional f32 bias (selection only), optional normalisation.
+ * workspace: at least vib3_router_workspace_bytes(num_experts) bytes, zeroed once before first
+ * use (vib3_hip_zero) and left ready for the next call. scores_out may be NULL. */
+size_t vib3_router_workspace_bytes(int num_experts);
+int vib3_launch_router_topk_ex(const void *hidden, int hidden_dtype, const void *router_weights,
+                               int weight_dtype, const float *bias, int hidden_dim,
+                               int num_experts, int top_k, int scoring_mode,
+                               float scaling_factor, int normalize, float *scores_out,
+                               uint16_t *out_ids, float *out_weights, void *workspace,
+                               void *stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Fused MoE layer for batch-1 decode over page-indexed INT4 experts: router -> device ids and
+ * weights -> page-table lookup -> fused gate/up GEMV + SwiGLU -> down GEMV with the weighted
+ * sum over experts in its epilogue. Three launches, no host synchronisation.
+ * Generalises vib3_launch_moe_experts_fused_gpu (cuda_ffi.rs:831, kernels.cu:5868): any number
+ * of pages per matrix, INT4 instead of NVFP4, shared experts in the same launches.
+ * ---------------------------------------------------------------------------------------- */
+
+#define VIB3_MOE_F32_INTERMEDIATE 1 /* keep h and the down outputs in f32 (no f16 rounding) */
+
+typedef struct vib3_moe_int4_layer {
+    /* activation: x[hidden] */
+    const void *x;
+    int x_dtype;
+    int hidden; /* k of gate/up, rows of down */
+    int inter;  /* rows of gate/up, k of down */
+    int group_size;
+    int scale_dtype;
+    /* router; when router_w is NULL the experts come from in_ids / in_weights (device) */
+    const void *router_w; /* [num_experts][hidden] */
+    int router_w_dtype;
+    const float *router_bias; /* [num_experts] or NULL */
+    int num_experts;
+    int top_k;
+    int scoring_mode;
+    float scaling_factor;
+    int normalize;
+    const uint16_t *in_ids;
+    const float *in_weights;
+    /* page tables (device): table[(expert * 3 + segment) * max_pages + page] = page address,
+     * segment 0 = up, 1 = gate, 2 = down (types.rs:200 PageId.segment). Page p of a segment
+     * holds rows [p * rows_per_page[seg], ...) of that matrix; the last page may be short. */
+    const uint64_t *page_table;
+    const uint64_t *shared_page_table; /* [num_shared][3][max_pages] or NULL */
+    int num_shared;
+    int max_pages;
+    int rows_per_page[3];
+    int flags;
+    /* outputs */
+    float *out;           /* [hidden] f32, overwritten: sum_j w_j * expert_j(x) + shared */
+    uint16_t *out_ids;    /* [top_k] or NULL */
+    float *out_weights;   /* [top_k] or NULL */
+    float *out_scores;    /* [num_experts] raw logits or NULL */
+    void *workspace;      /* vib3_moe_int4_workspace_bytes(), zeroed once (vib3_hip_zero) */
+    size_t workspace_bytes;
+} vib3_moe_int4_layer;
+
+size_t vib3_moe_int4_workspace_bytes(const vib3_moe_int4_layer *layer);
+int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer *layer, void *stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Utilities
+ * ---------------------------------------------------------------------------------------- */
+
+/* Zero `bytes` of device memory with a fill kernel (safe inside HIP graph capture). */
+int vib3_hip_zero(void *ptr, size_t bytes, void *stream);
+
+/* Synthetic data (no reference counterpart): counter-based generator whose spec is restated
+ * in the CPU oracle, so host and device produce identical bytes.
+ *   bytes:  byte j = (hash(seed, stream, j/8) >> 8*(j%8)) & 0xff for j in [off, off+n)
+ *   normal: Irwin-Hall(4) normal * sigma, written as dtype
+ *   int4 page: rows [row_start, row_start+rows) of the logical matrix `stream` (k, g). */
+int vib3_synth_bytes(void *dst, size_t n, uint64_t seed, uint64_t stream, size_t off,
+                     void *hip_stream);
+int vib3_synth_normal(void *dst, int dtype, size_t n, uint64_t seed, uint64_t stream,
+                      size_t off, float sigma, void *hip_stream);
+int vib3_synth_int4_page(void *page, uint64_t seed, uint64_t stream, int k, int group_size,
+                         int scale_dtype, float sigma, int row_start, int rows,
+                         void *hip_stream);
+
+/* Library version string. */
+const char *vib3_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,55 @@
+"""CPU-only checks of the C ABI: the library builds for gfx950, loads, and exports every symbol
+declared in include/vib3_hip.h; the ctypes table covers exactly those symbols. No kernel runs."""
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vib3_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(vib3_[a-z_0-9]+)\s*\(", text, re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_the_reference_launchers():
+    names = declared_functions()
+    for ref_name in ["vib3_launch_partial_matmul_int4", "vib3_launch_partial_matmul_int4_f32",
+                     "vib3_launch_fused_swiglu_int4_f32", "vib3_launch_silu_mul",
+                     "vib3_launch_weighted_accumulate_f32",
+                     "vib3_launch_weighted_accumulate_f32_f32", "vib3_launch_router_gemv_f32",
+                     "vib3_launch_router_topk"]:
+        assert ref_name in names
+
+
+def test_library_exports_every_declared_symbol():
+    from vib3_amd import _lib
+    lib_path = _lib.LIB_PATH
+    if not os.path.exists(lib_path):
+        from vib3_amd import build
+        build.build()
+    out = subprocess.run(["nm", "-D", "--defined-only", lib_path], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r" T (vib3_[a-z_0-9]+)$", out, re.M))
+    declared = set(declared_functions())
+    assert declared <= exported, declared - exported
+    assert set(_lib.SIGNATURES) == declared
+    lib = _lib.load()  # dlopen only; no GPU call
+    for name in declared:
+        assert getattr(lib, name)
+
+
+def test_code_object_targets_gfx950(tmp_path):
+    from vib3_amd import _lib
+    fb = tmp_path / "fatbin.bin"
+    subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", _lib.LIB_PATH,
+                    str(fb)], check=True)
+    out = subprocess.run(["/opt/rocm/lib/llvm/bin/clang-offload-bundler", "--list", "--type=o",
+                          f"--input={fb}"], capture_output=True, text=True, check=True)
+    targets = [t for t in out.stdout.split() if t.startswith("hip")]
+    assert targets == ["hipv4-amdgcn-amd-amdhsa--gfx950"]

@@ -1,0 +1,224 @@
+"""GPU parity of the fused MoE layer (vib3_launch_moe_int4_layer) against the CPU oracle.
+
+Configs follow BASELINE.json: c1 (Mixtral-shape layer, softmax top-2), c2 (Kimi-K2.5 layer,
+sigmoid top-8 + shared expert, all 385 experts resident), c3 (c2 paged into 64-row tiles at
+shuffled offsets of a 16 GB pool). Bar: router ids bit-exact where the selection margin exceeds
+1e-3, layer output rel-L2 <= 1e-3 against the oracle's reference-faithful composition (f16
+rounding of h and of each down output, as engine.rs does); paged == contiguous bit for bit.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+SEED = 0x5EED0002
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def check_layer(layer, bank, x, router_w_host, w_dt, bias_host, mode, scaling, k, faithful=True,
+                tol=1e-3, normalize=True):
+    from vib3_amd.moe import BankShape  # noqa: F401
+    sh = bank.shape
+    out = layer.launch(x).cpu().numpy()
+    torch.cuda.synchronize()
+    ids = layer.ids.cpu().numpy().view(np.uint16)[:k]
+    wts = layer.wts.cpu().numpy()[:k]
+    xh = x.float().cpu().numpy()
+    r_ids, r_wts, r_scores = O.router(xh, router_w_host, w_dt, sh.num_experts, sh.hidden, k, mode,
+                                      scaling, normalize, bias_host)
+    if mode == 1:
+        sig = 1 / (1 + np.exp(-r_scores.astype(np.float64)))
+        keys = sig + (bias_host if bias_host is not None else 0)
+    else:
+        keys = r_scores.astype(np.float64)
+    s = np.sort(keys)[::-1]
+    if k < sh.num_experts and s[k - 1] - s[k] <= 1e-3:
+        pytest.skip("selection margin below 1e-3 for this seed")
+    assert ids.tolist() == r_ids.tolist()
+    assert np.allclose(wts, r_wts, rtol=1e-5)
+    routed = {int(e): bank.expert_pages_host(int(e)) for e in r_ids}
+    shared = [bank.expert_pages_host(sh.num_experts + s) for s in range(sh.num_shared)]
+    ref = O.moe_layer(xh, sh.hidden, sh.inter, sh.group_size, sh.scale_dtype, routed, r_ids,
+                      r_wts, shared, faithful=faithful)
+    rel = rel_l2(out, ref)
+    _say(f"  rel_l2={rel:.3e}")
+    assert rel <= tol
+    return out, rel
+
+
+@pytest.fixture(scope="module")
+def kimi():
+    """c2: Kimi-K2.5 shape, 384 routed + 1 shared INT4 expert (g=32, bf16 scales)."""
+    from vib3_amd import moe
+    from vib3_amd._lib import DT_BF16
+    _say("setup: Kimi-K2.5 bank (385 experts, 9.5 GB)")
+    shape = moe.BankShape(hidden=7168, inter=2048, group_size=32, scale_dtype=DT_BF16,
+                          scale_sigma=0.01, num_experts=384, num_shared=1)
+    bank = moe.Int4ExpertBank(shape, layer=0, seed=SEED)
+    w, b = moe.make_router(shape, 0, SEED, 0.01, 0.1)
+    torch.cuda.synchronize()
+    return moe, shape, bank, w, b
+
+
+@pytest.mark.parametrize("token", [0, 1, 2])
+def test_c2_kimi_layer(kimi, token):
+    moe, shape, bank, w, b = kimi
+    from vib3_amd._lib import ROUTER_SIGMOID
+    _say(f"case: c2 kimi layer token={token}")
+    layer = moe.MoeInt4Layer(bank, w, b, top_k=8, scoring_mode=ROUTER_SIGMOID,
+                             scaling_factor=2.827, normalize=True)
+    x = moe.make_activation(shape.hidden, token, SEED)
+    out1, _ = check_layer(layer, bank, x, w.cpu().numpy(), O.F32, b.cpu().numpy(), 1, 2.827, 8)
+    out2 = layer.launch(x).cpu().numpy()
+    assert np.array_equal(out1, out2)  # deterministic: no atomics in the expert sum
+
+
+def test_c2_f32_intermediate(kimi):
+    moe, shape, bank, w, b = kimi
+    from vib3_amd._lib import MOE_F32_INTERMEDIATE, ROUTER_SIGMOID
+    _say("case: c2 f32 intermediate")
+    layer = moe.MoeInt4Layer(bank, w, b, top_k=8, scoring_mode=ROUTER_SIGMOID,
+                             scaling_factor=2.827, normalize=True, flags=MOE_F32_INTERMEDIATE)
+    x = moe.make_activation(shape.hidden, 5, SEED)
+    check_layer(layer, bank, x, w.cpu().numpy(), O.F32, b.cpu().numpy(), 1, 2.827, 8,
+                faithful=False, tol=1e-5)
+
+
+def test_c2_f32_activation(kimi):
+    """The engine feeds f32 normalised hidden states (engine.rs moe_normed_f32)."""
+    moe, shape, bank, w, b = kimi
+    from vib3_amd._lib import ROUTER_SIGMOID
+    _say("case: c2 f32 activation")
+    layer = moe.MoeInt4Layer(bank, w, b, top_k=8, scoring_mode=ROUTER_SIGMOID,
+                             scaling_factor=2.827, normalize=True)
+    x = moe.make_activation(shape.hidden, 6, SEED, dtype=torch.float32)
+    check_layer(layer, bank, x, w.cpu().numpy(), O.F32, b.cpu().numpy(), 1, 2.827, 8)
+
+
+def test_c3_paged_equals_contiguous(kimi):
+    """c3: the same logical matrices cut into 64-row tiles at shuffled offsets of a 16 GB pool
+    give bit-identical layer outputs (the page table only changes addresses)."""
+    moe, shape, bank, w, b = kimi
+    from vib3_amd._lib import ROUTER_SIGMOID
+    _say("case: c3 paged (16 GB pool)")
+    paged = moe.Int4ExpertBank(shape, layer=0, seed=SEED, layout="paged", tile_rows=64,
+                               pool_bytes=16 << 30)
+    assert paged.max_pages == 112 and paged.rows_per_page == [64, 64, 64]
+    lc = moe.MoeInt4Layer(bank, w, b, top_k=8, scoring_mode=ROUTER_SIGMOID, scaling_factor=2.827)
+    lp = moe.MoeInt4Layer(paged, w, b, top_k=8, scoring_mode=ROUTER_SIGMOID, scaling_factor=2.827)
+    for token in (0, 7):
+        x = moe.make_activation(shape.hidden, token, SEED)
+        a = lc.launch(x).cpu().numpy()
+        p = lp.launch(x).cpu().numpy()
+        assert np.array_equal(a, p)
+        assert np.array_equal(lc.ids.cpu().numpy(), lp.ids.cpu().numpy())
+    check_layer(lp, paged, moe.make_activation(shape.hidden, 9, SEED), w.cpu().numpy(), O.F32,
+                b.cpu().numpy(), 1, 2.827, 8)
+    del paged
+
+
+def test_c1_mixtral_layer():
+    """c1: Mixtral-shape layer: router fp32 [8, 4096], softmax top-2, 8 INT4 experts
+    (gate/up [14336, 4096], down [4096, 14336], g=128, fp16 scales), x fp16."""
+    from vib3_amd import moe
+    from vib3_amd._lib import DT_F16, ROUTER_SOFTMAX
+    _say("case: c1 mixtral layer")
+    shape = moe.BankShape(hidden=4096, inter=14336, group_size=128, scale_dtype=DT_F16,
+                          scale_sigma=0.02, num_experts=8, num_shared=0)
+    seed = 0x5EED0001
+    bank = moe.Int4ExpertBank(shape, layer=0, seed=seed)
+    w, _ = moe.make_router(shape, 0, seed, 0.02, None)
+    layer = moe.MoeInt4Layer(bank, w, None, top_k=2, scoring_mode=ROUTER_SOFTMAX)
+    for token in (0, 1):
+        x = moe.make_activation(shape.hidden, token, seed, dtype=torch.float16)
+        check_layer(layer, bank, x, w.cpu().numpy(), O.F32, None, 0, 1.0, 2)
+
+
+@pytest.mark.parametrize("layout,tile", [("contiguous", 0), ("paged", 64), ("paged", 96)])
+def test_small_layer_two_shared(layout, tile):
+    """Routed + 2 shared experts, sigmoid without normalisation, contiguous and paged."""
+    from vib3_amd import moe
+    from vib3_amd._lib import DT_BF16, ROUTER_SIGMOID
+    _say(f"case: small layer {layout} tile={tile}")
+    shape = moe.BankShape(hidden=1024, inter=256, group_size=32, scale_dtype=DT_BF16,
+                          scale_sigma=0.03, num_experts=40, num_shared=2)
+    bank = moe.Int4ExpertBank(shape, layer=3, seed=SEED, layout=layout, tile_rows=tile or 64,
+                              pool_bytes=64 << 20 if layout == "paged" else None)
+    w, bias = moe.make_router(shape, 3, SEED, 0.05, 0.1)
+    layer = moe.MoeInt4Layer(bank, w, bias, top_k=6, scoring_mode=ROUTER_SIGMOID,
+                             scaling_factor=1.5, normalize=False)
+    x = moe.make_activation(shape.hidden, 4, SEED)
+    check_layer(layer, bank, x, w.cpu().numpy(), O.F32, bias.cpu().numpy(), 1, 1.5, 6,
+                normalize=False)
+
+
+def test_ragged_rows_per_page():
+    """Pages of 48/40 rows: the last page of each matrix is short (engine pages from the
+    converter hold 520 / 1820 rows, convert.rs:1853-1865)."""
+    from vib3_amd import moe
+    from vib3_amd._lib import DT_BF16, ROUTER_SOFTMAX
+    _say("case: ragged rows per page")
+    shape = moe.BankShape(hidden=512, inter=160, group_size=32, scale_dtype=DT_BF16,
+                          scale_sigma=0.05, num_experts=6, num_shared=1)
+    for tile in (48, 40, 512):
+        bank = moe.Int4ExpertBank(shape, layer=1, seed=SEED, layout="paged", tile_rows=tile,
+                                  pool_bytes=32 << 20)
+        w, _ = moe.make_router(shape, 1, SEED, 0.05, None)
+        layer = moe.MoeInt4Layer(bank, w, None, top_k=3, scoring_mode=ROUTER_SOFTMAX)
+        x = moe.make_activation(shape.hidden, tile, SEED)
+        check_layer(layer, bank, x, w.cpu().numpy(), O.F32, None, 0, 1.0, 3)
+
+
+def test_given_ids_without_router():
+    """router_w == NULL: experts and weights come from the caller's device arrays (the shape of
+    moe_experts_fused_gpu, kernels.cu:5868)."""
+    from vib3_amd import moe
+    from vib3_amd._lib import DT_BF16
+    _say("case: given ids")
+    shape = moe.BankShape(hidden=1024, inter=512, group_size=32, scale_dtype=DT_BF16,
+                          scale_sigma=0.02, num_experts=12, num_shared=1)
+    bank = moe.Int4ExpertBank(shape, layer=2, seed=SEED)
+    layer = moe.MoeInt4Layer(bank, None, None, top_k=3, scoring_mode=0)
+    ids = np.array([11, 0, 5], dtype=np.uint16)
+    wts = np.array([0.5, 0.25, 1.25], dtype=np.float32)
+    x = moe.make_activation(shape.hidden, 0, SEED)
+    out = layer.launch(x, torch.from_numpy(ids.view(np.int16)).cuda(),
+                       torch.from_numpy(wts).cuda()).cpu().numpy()
+    routed = {int(e): bank.expert_pages_host(int(e)) for e in ids}
+    ref = O.moe_layer(x.float().cpu().numpy(), shape.hidden, shape.inter, 32, O.BF16, routed, ids,
+                      wts, [bank.expert_pages_host(12)], faithful=True)
+    assert rel_l2(out, ref) <= 1e-3
+
+
+def test_layer_argument_errors():
+    from vib3_amd import _lib, moe
+    from vib3_amd._lib import DT_BF16
+    _say("case: layer argument errors")
+    shape = moe.BankShape(hidden=1024, inter=256, num_experts=4, num_shared=0,
+                          scale_dtype=DT_BF16)
+    bank = moe.Int4ExpertBank(shape, layer=0, seed=SEED)
+    layer = moe.MoeInt4Layer(bank, None, None, top_k=2, scoring_mode=0)
+    x = moe.make_activation(shape.hidden, 0, SEED)
+    with pytest.raises(_lib.Vib3Error):  # neither router nor ids given
+        layer.launch(x)
+    d = layer._desc(x)
+    d.workspace_bytes = 16
+    assert _lib.load().vib3_launch_moe_int4_layer(d, None) == -4
+    d = layer._desc(x)
+    d.top_k = 17
+    assert _lib.load().vib3_launch_moe_int4_layer(d, None) == -2

@@ -1,0 +1,328 @@
+// api.hip — the C ABI of libvib3_hip (include/vib3_hip.h): argument checks, workspace layout
+// and launch sequences. All entry points are asynchronous on the caller's stream, allocate
+// nothing and keep no mutable global state, so they are reentrant across streams.
+#include <string.h>
+
+#include "common.h"
+#include "kernels.h"
+
+using namespace vib3;
+
+namespace {
+
+inline hipStream_t S(void* p) { return (hipStream_t)p; }
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+inline bool valid_act_dt(int dt) { return dt == VIB3_DT_F32 || dt == VIB3_DT_F16 || dt == VIB3_DT_BF16; }
+inline bool valid_scale_dt(int dt) { return dt == VIB3_DT_F16 || dt == VIB3_DT_BF16; }
+inline bool valid_out_dt(int dt) { return dt == VIB3_DT_F32 || dt == VIB3_DT_F16; }
+inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// One flat INT4 matrix (or up/gate pair) times a vector: the fast kernel when the shape and
+// alignment allow 16-byte chunk loads, otherwise the generic kernel.
+int int4_flat(const void* x, int x_dt, const void* d0, const void* s0, const void* d1,
+              const void* s1, void* out, int out_dt, int k, int m, int g, int sdt, bool dual,
+              hipStream_t st) {
+  if (k <= 0 || m < 0 || g <= 0) return VIB3_ERR_BAD_COUNT;
+  if (!x || !d0 || !s0 || !out || (dual && (!d1 || !s1))) return VIB3_ERR_BAD_POINTER;
+  if (m == 0) return 0;
+  const bool fast = (k % 32 == 0) && (k / 32 <= 16 * kWave) && aligned16(d0) &&
+                    (!dual || aligned16(d1)) && aligned16(x) && ((uintptr_t)s0 % 2 == 0) &&
+                    (!dual || (uintptr_t)s1 % 2 == 0);
+  if (fast) {
+    RowsArgs a{};
+    a.x = x; a.x_dt = x_dt; a.K = k; a.M = m; a.g = g; a.sdt = sdt; a.nslots = 1;
+    a.flat0 = MatRef{nullptr, (const uint8_t*)d0, (const uint16_t*)s0, 0, m};
+    a.flat1 = dual ? MatRef{nullptr, (const uint8_t*)d1, (const uint16_t*)s1, 0, m} : a.flat0;
+    a.out = out; a.out_dt = out_dt; a.out_stride = 0;
+    return launch_rows(a, dual, st);
+  }
+  GenericArgs a{x, x_dt, k, m, g, sdt, (const uint8_t*)d0, (const uint16_t*)s0,
+                (const uint8_t*)d1, (const uint16_t*)s1, out, out_dt};
+  return launch_generic(a, dual, st);
+}
+
+inline const void* scales_of(const void* page, int k, int m) {
+  return (const uint8_t*)page + (size_t)((k + 1) / 2) * (size_t)m;
+}
+
+__global__ void k_silu_mul(const uint16_t* a, const uint16_t* b, uint16_t* out, int n) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i >= n) return;
+  const float g = f16_to_f32(a[i]);
+  out[i] = f32_to_f16_bits((g / (1.0f + expf(-g))) * f16_to_f32(b[i]));
+}
+
+__global__ void k_weighted_acc(float* out, const void* e, int e_f32, float w, int n) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i >= n) return;
+  const float v = e_f32 ? ((const float*)e)[i] : f16_to_f32(((const uint16_t*)e)[i]);
+  out[i] = __fadd_rn(out[i], __fmul_rn(w, v));
+}
+
+__global__ void k_zero(uint4* p16, size_t n16, uint8_t* tail, size_t ntail) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n16) p16[i] = make_uint4(0, 0, 0, 0);
+  if (i < ntail) tail[i] = 0;
+}
+
+// Workspace of the fused layer: [counter | scores[E] | ids[k] | wts[k] | h[nslots][inter]].
+struct LayerWs {
+  size_t counter, scores, ids, wts, h, total;
+};
+
+LayerWs layer_ws(const vib3_moe_int4_layer* L) {
+  LayerWs w{};
+  const int nslots = L->top_k + L->num_shared;
+  const size_t hsz = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? 4 : 2;
+  w.counter = 0;
+  w.scores = 256;
+  w.ids = round_up(w.scores + 4 * (size_t)(L->num_experts > 0 ? L->num_experts : 0), 256);
+  w.wts = round_up(w.ids + 2 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
+  w.h = round_up(w.wts + 4 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
+  w.total = round_up(w.h + hsz * (size_t)(nslots > 0 ? nslots : 0) * (size_t)(L->inter > 0 ? L->inter : 0), 256);
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* vib3_hip_version(void) { return "vib3_hip 0.1 gfx950"; }
+
+int vib3_hip_zero(void* ptr, size_t bytes, void* stream) {
+  if (!ptr) return VIB3_ERR_BAD_POINTER;
+  if (bytes == 0) return 0;
+  size_t n16 = aligned16(ptr) ? bytes / 16 : 0;
+  uint8_t* tail = (uint8_t*)ptr + n16 * 16;
+  size_t ntail = bytes - n16 * 16;
+  size_t n = n16 > ntail ? n16 : ntail;
+  hipLaunchKernelGGL(k_zero, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, S(stream),
+                     (uint4*)ptr, n16, tail, ntail);
+  VIB3_RETURN_LAUNCH();
+}
+
+// ---------------------------------------------------------------- reference-compatible
+
+int vib3_launch_partial_matmul_int4(const void* input, const void* weight_packed,
+                                    const void* scales, void* output, int k, int m_slice,
+                                    int group_size, void* stream) {
+  return int4_flat(input, VIB3_DT_F16, weight_packed, scales, nullptr, nullptr, output,
+                   VIB3_DT_F16, k, m_slice, group_size, VIB3_DT_F16, false, S(stream));
+}
+
+int vib3_launch_partial_matmul_int4_f32(const void* input, const void* weight, const void* scales,
+                                        void* output, int k, int m_slice, int group_size,
+                                        void* stream) {
+  return int4_flat(input, VIB3_DT_F32, weight, scales, nullptr, nullptr, output, VIB3_DT_F16, k,
+                   m_slice, group_size, VIB3_DT_F16, false, S(stream));
+}
+
+int vib3_launch_fused_swiglu_int4_f32(const void* input, const void* up_weight,
+                                      const void* up_scales, const void* gate_weight,
+                                      const void* gate_scales, void* output, int k, int m_slice,
+                                      int group_size, void* stream) {
+  return int4_flat(input, VIB3_DT_F32, up_weight, up_scales, gate_weight, gate_scales, output,
+                   VIB3_DT_F16, k, m_slice, group_size, VIB3_DT_F16, true, S(stream));
+}
+
+int vib3_launch_silu_mul(const void* up_result, const void* gate_result, void* output, int dim,
+                         void* stream) {
+  if (dim < 0) return VIB3_ERR_BAD_COUNT;
+  if (!up_result || !gate_result || !output) return VIB3_ERR_BAD_POINTER;
+  if (dim == 0) return 0;
+  hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0, S(stream),
+                     (const uint16_t*)up_result, (const uint16_t*)gate_result, (uint16_t*)output,
+                     dim);
+  VIB3_RETURN_LAUNCH();
+}
+
+int vib3_launch_weighted_accumulate_f32(void* output, const void* expert_output, float weight,
+                                        int dim, void* stream) {
+  if (dim < 0) return VIB3_ERR_BAD_COUNT;
+  if (!output || !expert_output) return VIB3_ERR_BAD_POINTER;
+  if (dim == 0) return 0;
+  hipLaunchKernelGGL(k_weighted_acc, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0,
+                     S(stream), (float*)output, expert_output, 0, weight, dim);
+  VIB3_RETURN_LAUNCH();
+}
+
+int vib3_launch_weighted_accumulate_f32_f32(void* output, const void* expert_output,
+                                            float weight, int dim, void* stream) {
+  if (dim < 0) return VIB3_ERR_BAD_COUNT;
+  if (!output || !expert_output) return VIB3_ERR_BAD_POINTER;
+  if (dim == 0) return 0;
+  hipLaunchKernelGGL(k_weighted_acc, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0,
+                     S(stream), (float*)output, expert_output, 1, weight, dim);
+  VIB3_RETURN_LAUNCH();
+}
+
+int vib3_launch_router_gemv_f32(const void* hidden_state, const void* router_weights,
+                                float* scores, int hidden_dim, int num_experts, void* stream) {
+  if (hidden_dim <= 0 || num_experts <= 0) return VIB3_ERR_BAD_COUNT;
+  if (!hidden_state || !router_weights || !scores) return VIB3_ERR_BAD_POINTER;
+  RouterArgs a{};
+  a.x = hidden_state; a.x_dt = VIB3_DT_F32; a.w = router_weights; a.w_dt = VIB3_DT_F16;
+  a.D = hidden_dim; a.E = num_experts; a.scores = scores;
+  return launch_router_logits(a, S(stream));
+}
+
+int vib3_launch_router_topk(const void* hidden_state, const void* router_weights,
+                            float* scores_buf, const float* bias, uint16_t* out_ids,
+                            float* out_weights, int hidden_dim, int num_experts, int top_k,
+                            int scoring_mode, float scaling_factor, void* stream) {
+  if (hidden_dim <= 0 || num_experts <= 0 || num_experts > kMaxExperts || top_k <= 0 ||
+      top_k > num_experts || top_k > 64)
+    return VIB3_ERR_BAD_COUNT;
+  if (scoring_mode != VIB3_ROUTER_SOFTMAX && scoring_mode != VIB3_ROUTER_SIGMOID)
+    return VIB3_ERR_UNSUPPORTED;
+  if (!hidden_state || !router_weights || !scores_buf || !out_ids || !out_weights)
+    return VIB3_ERR_BAD_POINTER;
+  RouterArgs a{};
+  a.x = hidden_state; a.x_dt = VIB3_DT_F32; a.w = router_weights; a.w_dt = VIB3_DT_F16;
+  a.bias = bias; a.D = hidden_dim; a.E = num_experts; a.top_k = top_k; a.mode = scoring_mode;
+  a.scaling = scoring_mode == VIB3_ROUTER_SIGMOID ? scaling_factor : 1.0f;
+  a.normalize = 1;  // the reference GPU kernel always normalises (kernels.cu:4056)
+  a.scores = scores_buf; a.ids = out_ids; a.wts = out_weights;
+  int rc = launch_router_logits(a, S(stream));
+  if (rc) return rc;
+  return launch_router_select(a, S(stream));
+}
+
+// ---------------------------------------------------------------- additive
+
+int vib3_launch_partial_matmul_int4_ex(const void* input, int input_dtype, const void* weight_page,
+                                       void* output, int output_dtype, int k, int m_slice,
+                                       int group_size, int scale_dtype, void* stream) {
+  if (!valid_act_dt(input_dtype) || !valid_out_dt(output_dtype) || !valid_scale_dt(scale_dtype))
+    return VIB3_ERR_UNSUPPORTED;
+  if (k <= 0 || m_slice < 0) return VIB3_ERR_BAD_COUNT;
+  return int4_flat(input, input_dtype, weight_page, scales_of(weight_page, k, m_slice), nullptr,
+                   nullptr, output, output_dtype, k, m_slice, group_size, scale_dtype, false,
+                   S(stream));
+}
+
+int vib3_launch_partial_swiglu_int4_ex(const void* input, int input_dtype, const void* up_page,
+                                       const void* gate_page, void* output, int output_dtype,
+                                       int k, int m_slice, int group_size, int scale_dtype,
+                                       void* stream) {
+  if (!valid_act_dt(input_dtype) || !valid_out_dt(output_dtype) || !valid_scale_dt(scale_dtype))
+    return VIB3_ERR_UNSUPPORTED;
+  if (k <= 0 || m_slice < 0) return VIB3_ERR_BAD_COUNT;
+  return int4_flat(input, input_dtype, up_page, scales_of(up_page, k, m_slice), gate_page,
+                   scales_of(gate_page, k, m_slice), output, output_dtype, k, m_slice, group_size,
+                   scale_dtype, true, S(stream));
+}
+
+size_t vib3_router_workspace_bytes(int num_experts) {
+  return 256 + round_up(4 * (size_t)(num_experts > 0 ? num_experts : 0), 256) + 256 + 512;
+}
+
+int vib3_launch_router_topk_ex(const void* hidden, int hidden_dtype, const void* router_weights,
+                               int weight_dtype, const float* bias, int hidden_dim,
+                               int num_experts, int top_k, int scoring_mode, float scaling_factor,
+                               int normalize, float* scores_out, uint16_t* out_ids,
+                               float* out_weights, void* workspace, void* stream) {
+  if (!valid_act_dt(hidden_dtype) || !valid_act_dt(weight_dtype)) return VIB3_ERR_UNSUPPORTED;
+  if (scoring_mode != VIB3_ROUTER_SOFTMAX && scoring_mode != VIB3_ROUTER_SIGMOID)
+    return VIB3_ERR_UNSUPPORTED;
+  if (hidden_dim <= 0 || num_experts <= 0 || num_experts > kMaxExperts || top_k <= 0 ||
+      top_k > num_experts || top_k > 64)
+    return VIB3_ERR_BAD_COUNT;
+  if (!hidden || !router_weights || !workspace) return VIB3_ERR_BAD_POINTER;
+  char* ws = (char*)workspace;
+  const size_t sc = 256, ids = sc + round_up(4 * (size_t)num_experts, 256), wts = ids + 256;
+  RouterArgs a{};
+  a.x = hidden; a.x_dt = hidden_dtype; a.w = router_weights; a.w_dt = weight_dtype;
+  a.bias = bias; a.D = hidden_dim; a.E = num_experts; a.top_k = top_k; a.mode = scoring_mode;
+  a.scaling = scoring_mode == VIB3_ROUTER_SIGMOID ? scaling_factor : 1.0f;
+  a.normalize = normalize;
+  a.counter = (unsigned*)ws;
+  a.scores = scores_out ? scores_out : (float*)(ws + sc);
+  a.ids = (uint16_t*)(ws + ids);
+  a.wts = (float*)(ws + wts);
+  a.out_ids = out_ids;
+  a.out_wts = out_weights;
+  return launch_router_fused(a, S(stream));
+}
+
+size_t vib3_moe_int4_workspace_bytes(const vib3_moe_int4_layer* L) {
+  if (!L) return 0;
+  return layer_ws(L).total;
+}
+
+int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
+  if (!L) return VIB3_ERR_BAD_POINTER;
+  if (!valid_act_dt(L->x_dtype) || !valid_scale_dt(L->scale_dtype)) return VIB3_ERR_UNSUPPORTED;
+  if (L->hidden <= 0 || L->inter <= 0 || L->group_size <= 0 || L->top_k < 0 ||
+      L->num_shared < 0 || L->max_pages <= 0)
+    return VIB3_ERR_BAD_COUNT;
+  const int nslots = L->top_k + L->num_shared;
+  if (nslots <= 0 || nslots > 16 || L->top_k > 64) return VIB3_ERR_BAD_COUNT;
+  if (L->hidden % 32 || L->inter % 32) return VIB3_ERR_UNSUPPORTED;
+  for (int s = 0; s < 3; s++)
+    if (L->rows_per_page[s] <= 0) return VIB3_ERR_BAD_COUNT;
+  if ((L->rows_per_page[0] + 0LL) * L->max_pages < L->inter ||
+      (L->rows_per_page[1] + 0LL) * L->max_pages < L->inter ||
+      (L->rows_per_page[2] + 0LL) * L->max_pages < L->hidden)
+    return VIB3_ERR_BAD_COUNT;
+  if (!L->x || !L->out || !L->workspace || (L->top_k > 0 && !L->page_table) ||
+      (L->num_shared > 0 && !L->shared_page_table) || !aligned16(L->x) ||
+      !aligned16(L->workspace))
+    return VIB3_ERR_BAD_POINTER;
+  const LayerWs w = layer_ws(L);
+  if (L->workspace_bytes < w.total) return VIB3_ERR_WORKSPACE;
+  char* ws = (char*)L->workspace;
+  hipStream_t st = S(stream);
+
+  const uint16_t* ids = (const uint16_t*)(ws + w.ids);
+  const float* wts = (const float*)(ws + w.wts);
+  if (L->top_k > 0) {
+    if (L->router_w) {
+      if (!valid_act_dt(L->router_w_dtype)) return VIB3_ERR_UNSUPPORTED;
+      if (L->num_experts <= 0 || L->num_experts > kMaxExperts || L->top_k > L->num_experts)
+        return VIB3_ERR_BAD_COUNT;
+      if (L->scoring_mode != VIB3_ROUTER_SOFTMAX && L->scoring_mode != VIB3_ROUTER_SIGMOID)
+        return VIB3_ERR_UNSUPPORTED;
+      RouterArgs r{};
+      r.x = L->x; r.x_dt = L->x_dtype; r.w = L->router_w; r.w_dt = L->router_w_dtype;
+      r.bias = L->router_bias; r.D = L->hidden; r.E = L->num_experts; r.top_k = L->top_k;
+      r.mode = L->scoring_mode;
+      r.scaling = L->scoring_mode == VIB3_ROUTER_SIGMOID ? L->scaling_factor : 1.0f;
+      r.normalize = L->normalize;
+      r.counter = (unsigned*)(ws + w.counter);
+      r.scores = L->out_scores ? L->out_scores : (float*)(ws + w.scores);
+      r.ids = (uint16_t*)(ws + w.ids);
+      r.wts = (float*)(ws + w.wts);
+      r.out_ids = L->out_ids;
+      r.out_wts = L->out_weights;
+      int rc = launch_router_fused(r, st);
+      if (rc) return rc;
+    } else {
+      if (!L->in_ids || !L->in_weights) return VIB3_ERR_BAD_POINTER;
+      ids = L->in_ids;
+      wts = L->in_weights;
+    }
+  }
+
+  const int h_dt = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? VIB3_DT_F32 : VIB3_DT_F16;
+  RowsArgs a{};
+  a.x = L->x; a.x_dt = L->x_dtype; a.K = L->hidden; a.M = L->inter; a.g = L->group_size;
+  a.sdt = L->scale_dtype; a.nslots = nslots;
+  a.routed_table = L->page_table; a.shared_table = L->shared_page_table; a.ids = ids;
+  a.top_k = L->top_k; a.max_pages = L->max_pages;
+  a.rpp[0] = L->rows_per_page[0]; a.rpp[1] = L->rows_per_page[1]; a.rpp[2] = L->rows_per_page[2];
+  a.out = ws + w.h; a.out_dt = h_dt; a.out_stride = (size_t)L->inter;
+  int rc = launch_rows(a, true, st);
+  if (rc) return rc;
+
+  DownArgs d{};
+  d.h = ws + w.h; d.h_dt = h_dt; d.K = L->inter; d.M = L->hidden; d.g = L->group_size;
+  d.sdt = L->scale_dtype; d.nslots = nslots; d.routed_table = L->page_table;
+  d.shared_table = L->shared_page_table; d.ids = ids; d.wts = wts; d.top_k = L->top_k;
+  d.max_pages = L->max_pages; d.rpp = L->rows_per_page[2];
+  d.round_f16 = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? 0 : 1;
+  d.out = L->out;
+  return launch_down(d, st);
+}
+
+}  // extern "C"

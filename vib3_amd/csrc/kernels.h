@@ -1,0 +1,93 @@
+// kernels.h — argument blocks and internal launchers shared by the .hip translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace vib3 {
+
+// Rows of one matrix (or of the up/gate pair) per expert slot. Slot s of a paged launch reads
+// expert ids[s] from routed_table for s < top_k and shared expert s - top_k from shared_table;
+// a flat launch (routed_table == nullptr, one slot) reads flat0 / flat1.
+struct RowsArgs {
+  const void* x;
+  int x_dt;
+  int K, M, g, sdt;
+  int nslots;
+  const uint64_t* routed_table;
+  const uint64_t* shared_table;
+  const uint16_t* ids;
+  int top_k;
+  int max_pages;
+  int rpp[3];
+  MatRef flat0, flat1;
+  void* out;
+  int out_dt;
+  size_t out_stride;  // elements between slots in out
+  int KS;             // waves that split one row's k range (set by the launcher)
+  int RPT;            // rows per team
+};
+
+// Down projection of every slot for a block of RB output rows plus the weighted expert sum.
+struct DownArgs {
+  const void* h;  // [nslots][K] intermediate, f16 or f32
+  int h_dt;
+  int K, M, g, sdt;
+  int nslots;
+  const uint64_t* routed_table;
+  const uint64_t* shared_table;
+  const uint16_t* ids;
+  const float* wts;
+  int top_k;
+  int max_pages;
+  int rpp;  // rows per page of the down segment
+  int KS;
+  int RB;
+  int round_f16;
+  float* out;
+};
+
+struct GenericArgs {
+  const void* x;
+  int x_dt;
+  int K, M, g, sdt;
+  const uint8_t* data0;
+  const uint16_t* scales0;
+  const uint8_t* data1;
+  const uint16_t* scales1;
+  void* out;
+  int out_dt;
+};
+
+int launch_rows(RowsArgs a, bool dual, hipStream_t s);
+int launch_down(DownArgs a, hipStream_t s);
+int launch_generic(GenericArgs a, bool dual, hipStream_t s);
+
+// Router: logits (one workgroup per expert) and, when fused, top-k selection by the last
+// workgroup to finish. ws_* are device buffers of the caller's workspace.
+struct RouterArgs {
+  const void* x;
+  int x_dt;
+  const void* w;
+  int w_dt;
+  const float* bias;
+  int D, E, top_k, mode;
+  float scaling;
+  int normalize;
+  float* scores;       // [E] logits (workspace or caller)
+  unsigned* counter;   // completion counter (fused only), zero between launches
+  uint16_t* ids;       // [top_k] selection (workspace)
+  float* wts;          // [top_k]
+  uint16_t* out_ids;   // optional copies for the caller
+  float* out_wts;
+};
+
+int launch_router_fused(const RouterArgs& a, hipStream_t s);
+int launch_router_logits(const RouterArgs& a, hipStream_t s);
+int launch_router_select(const RouterArgs& a, hipStream_t s);
+
+constexpr int kMaxExperts = 4096;
+
+}  // namespace vib3

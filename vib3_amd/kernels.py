@@ -1,0 +1,194 @@
+"""Host mirror of vib3's launcher API (src/compute/kernels.rs) over libvib3_hip.
+
+Same function names, argument meaning and error behaviour as the reference launchers, with
+torch tensors standing in for raw device pointers (``tensor.data_ptr()`` is what crosses the C
+ABI). Every call runs the HIP kernels on the current torch stream of the tensor's device;
+there is no CPU branch — a missing library or a CPU tensor raises.
+
+Scale dtype: the reference CPU fallback decodes INT4 group scales as BF16
+(kernels.rs:2789) while its GPU kernels decode FP16 (kernels.cu:45, :140). The functions here
+take ``scale_dtype`` (default BF16, the CPU-fallback semantics the parity tests hold them to);
+the reference GPU behaviour is ``scale_dtype=DT_F16``.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List, Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import DT_BF16, DT_F16, DT_F32, ROUTER_SIGMOID, ROUTER_SOFTMAX
+
+INT4_GROUP_SIZE = 32  # kernels.rs:3737
+
+
+class DType:
+    """Subset of core/types.rs:633 DType used by the expert path."""
+
+    FP16 = 1
+    BF16 = 2
+    INT4 = 5
+    NVFP4 = 7
+
+
+@dataclass(frozen=True)
+class Softmax:
+    """kernels.rs:2226 RouterScoringFunc::Softmax."""
+
+
+@dataclass(frozen=True)
+class Sigmoid:
+    """kernels.rs:2226 RouterScoringFunc::Sigmoid { scaling_factor, normalize }."""
+
+    scaling_factor: float = 1.0
+    normalize: bool = True
+
+
+RouterScoringFunc = object  # Softmax() | Sigmoid(...)
+
+_TORCH_DT = {torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16}
+
+
+def _dev(t: torch.Tensor, name: str) -> int:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a device tensor (no CPU fallback in vib3_amd)")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t.data_ptr()
+
+
+def _act_dt(t: torch.Tensor, name: str) -> int:
+    if t.dtype not in _TORCH_DT:
+        raise TypeError(f"{name}: unsupported dtype {t.dtype}")
+    return _TORCH_DT[t.dtype]
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need_int4(weight_dtype: int) -> None:
+    if weight_dtype != DType.INT4:
+        raise NotImplementedError("vib3_amd implements the INT4 expert path (DType.INT4)")
+
+
+def partial_matmul(input: torch.Tensor, weight_page: torch.Tensor, output: torch.Tensor, k: int,
+                   m_slice: int, weight_dtype: int = DType.INT4, group_size: int = INT4_GROUP_SIZE,
+                   scale_dtype: int = DT_BF16) -> None:
+    """kernels.rs:25 partial_matmul: output[m_slice] = weight_page[m_slice, k] . input[k].
+
+    input f32/f16/bf16; output f16 or f32; weight_page = [m*ceil(k/2) nibbles][m*G*2 scales]."""
+    _need_int4(weight_dtype)
+    _lib.call("vib3_launch_partial_matmul_int4_ex", _dev(input, "input"), _act_dt(input, "input"),
+              _dev(weight_page, "weight_page"), _dev(output, "output"),
+              _act_dt(output, "output"), k, m_slice, group_size, scale_dtype, _stream(input))
+
+
+def partial_matmul_f32(input, weight_page, output, k, m_slice, weight_dtype=DType.INT4,
+                       group_size=INT4_GROUP_SIZE, scale_dtype=DT_BF16) -> None:
+    """kernels.rs:375 partial_matmul_f32 (f32 input)."""
+    if input.dtype != torch.float32:
+        raise TypeError("partial_matmul_f32 takes an f32 input")
+    partial_matmul(input, weight_page, output, k, m_slice, weight_dtype, group_size, scale_dtype)
+
+
+def partial_swiglu(input: torch.Tensor, up_page: torch.Tensor, gate_page: torch.Tensor,
+                   output: torch.Tensor, hidden_dim: int, m_slice: int,
+                   weight_dtype: int = DType.INT4, swiglu_temps=None,
+                   group_size: int = INT4_GROUP_SIZE, scale_dtype: int = DT_BF16) -> None:
+    """kernels.rs:162 partial_swiglu: output = silu(gate . input) * (up . input), one launch.
+
+    ``swiglu_temps`` is accepted for signature compatibility and unused: the fused kernel has no
+    intermediates."""
+    _need_int4(weight_dtype)
+    _lib.call("vib3_launch_partial_swiglu_int4_ex", _dev(input, "input"), _act_dt(input, "input"),
+              _dev(up_page, "up_page"), _dev(gate_page, "gate_page"), _dev(output, "output"),
+              _act_dt(output, "output"), hidden_dim, m_slice, group_size, scale_dtype,
+              _stream(input))
+
+
+def partial_swiglu_f32(input, up_page, gate_page, output, hidden_dim, m_slice,
+                       weight_dtype=DType.INT4, swiglu_temps=None, group_size=INT4_GROUP_SIZE,
+                       scale_dtype=DT_BF16) -> None:
+    """kernels.rs:459 partial_swiglu_f32 (f32 input)."""
+    if input.dtype != torch.float32:
+        raise TypeError("partial_swiglu_f32 takes an f32 input")
+    partial_swiglu(input, up_page, gate_page, output, hidden_dim, m_slice, weight_dtype,
+                   swiglu_temps, group_size, scale_dtype)
+
+
+def weighted_accumulate_f32(output: torch.Tensor, expert_output: torch.Tensor, weight: float,
+                            dim: int) -> None:
+    """kernels.rs:2000 weighted_accumulate_f32: output_f32 += weight * expert_output (f16/f32)."""
+    if output.dtype != torch.float32:
+        raise TypeError("output must be f32")
+    name = ("vib3_launch_weighted_accumulate_f32" if expert_output.dtype == torch.float16
+            else "vib3_launch_weighted_accumulate_f32_f32")
+    if expert_output.dtype not in (torch.float16, torch.float32):
+        raise TypeError("expert_output must be f16 or f32")
+    _lib.call(name, _dev(output, "output"), _dev(expert_output, "expert_output"), float(weight),
+              dim, _stream(output))
+
+
+def _scoring(scoring_func) -> Tuple[int, float, int]:
+    if isinstance(scoring_func, Sigmoid):
+        return ROUTER_SIGMOID, float(scoring_func.scaling_factor), int(scoring_func.normalize)
+    if isinstance(scoring_func, Softmax) or scoring_func is None:
+        return ROUTER_SOFTMAX, 1.0, 1
+    raise TypeError(f"unknown scoring function {scoring_func!r}")
+
+
+class RouterWorkspace:
+    """Device workspace of the one-launch router (completion counter + scratch), zeroed once."""
+
+    def __init__(self, num_experts: int, device) -> None:
+        n = _lib.load().vib3_router_workspace_bytes(num_experts)
+        self.buf = torch.zeros(n, dtype=torch.uint8, device=device)
+        self.num_experts = num_experts
+
+
+def run_router_gpu_topk_nosync(hidden_state: torch.Tensor, router_weights: torch.Tensor,
+                               num_experts: int, hidden_dim: int, top_k: int, scoring_func,
+                               topk_ids_dev: torch.Tensor, topk_weights_dev: torch.Tensor,
+                               correction_bias: Optional[torch.Tensor] = None,
+                               scores_dev: Optional[torch.Tensor] = None,
+                               workspace: Optional[RouterWorkspace] = None) -> None:
+    """kernels.rs:1890 run_router_gpu_topk_nosync: ids/weights stay on the device."""
+    mode, scale, norm = _scoring(scoring_func)
+    if workspace is None or workspace.num_experts < num_experts:
+        workspace = RouterWorkspace(num_experts, hidden_state.device)
+    if topk_ids_dev.dtype not in (torch.int16, torch.uint16):
+        raise TypeError("topk_ids_dev must be a 16-bit tensor")
+    bias_p = _dev(correction_bias, "correction_bias") if correction_bias is not None else None
+    scores_p = _dev(scores_dev, "scores_dev") if scores_dev is not None else None
+    _lib.call("vib3_launch_router_topk_ex", _dev(hidden_state, "hidden_state"),
+              _act_dt(hidden_state, "hidden_state"), _dev(router_weights, "router_weights"),
+              _act_dt(router_weights, "router_weights"), bias_p, hidden_dim, num_experts, top_k,
+              mode, scale, norm, scores_p, _dev(topk_ids_dev, "topk_ids_dev"),
+              _dev(topk_weights_dev, "topk_weights_dev"), workspace.buf.data_ptr(),
+              _stream(hidden_state))
+
+
+def run_router_with_scoring_and_bias(hidden_state: torch.Tensor, router_weights: torch.Tensor,
+                                     num_experts: int, hidden_dim: int, top_k: int,
+                                     scoring_func=Softmax(), scores_dev=None,
+                                     correction_bias: Optional[torch.Tensor] = None,
+                                     workspace: Optional[RouterWorkspace] = None
+                                     ) -> List[Tuple[int, float]]:
+    """kernels.rs:2307: route on the device, then copy the k (id, weight) pairs to the host
+    (one small D2H, as run_router_gpu_topk does at kernels.rs:1859-1873)."""
+    dev = hidden_state.device
+    ids = torch.empty(top_k, dtype=torch.int16, device=dev)
+    wts = torch.empty(top_k, dtype=torch.float32, device=dev)
+    run_router_gpu_topk_nosync(hidden_state, router_weights, num_experts, hidden_dim, top_k,
+                               scoring_func, ids, wts, correction_bias, scores_dev, workspace)
+    ids_h = ids.cpu().numpy().view("uint16").tolist()
+    return list(zip(ids_h, wts.cpu().tolist()))
+
+
+def run_router_gpu_topk(hidden_state, router_weights, num_experts, hidden_dim, top_k,
+                        scoring_func, scores_dev=None, topk_ids_dev=None, topk_weights_dev=None):
+    """kernels.rs:1811 run_router_gpu_topk (bias always NULL there)."""
+    return run_router_with_scoring_and_bias(hidden_state, router_weights, num_experts, hidden_dim,
+                                            top_k, scoring_func, scores_dev)
