@@ -1,0 +1,266 @@
+"""Benchmark: MoE layer decode (batch 1, Kimi-K2.5 shape) on one MI355X.
+
+A step = one full MoE sublayer decode for one token over experts resident in HBM: router
+(384 experts, fp32 weights, sigmoid + bias, top-8, normalised, x2.827) -> fused INT4 gate/up GEMV
++ SwiGLU over the 8 routed + 1 shared experts -> INT4 down GEMV with the weighted expert sum.
+Workload = BASELINE.json configs[2] (c2); --config c3 runs the paged variant (64-row tiles at
+shuffled offsets of a 16 GB pool), --config c1 the Mixtral-shape layer.
+
+Every step uses a different token and the steps rotate over `--layers` independent layers
+(separate router and expert weights), so the weights a step reads were last touched
+>= layers * 234 MB earlier and are not served from the 256 MB last-level cache: the timed
+bytes come from HBM, as in a real decode that walks through 61 layers.
+
+Prints ONE JSON line (rank 0). `value` = microseconds per layer (lower is better).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+CONFIGS = {
+    "c2": dict(workload="c2: Kimi-K2.5 MoE layer decode, batch 1 (router fp32 [384,7168] sigmoid+bias "
+                        "top-8 x2.827 normalised; 8 routed + 1 shared INT4 experts, hidden 7168, "
+                        "inter 2048, g32 bf16 scales; x bf16)",
+               hidden=7168, inter=2048, g=32, sdt="bf16", sigma=0.01, E=384, shared=1, k=8,
+               mode=1, scaling=2.827, router_sigma=0.01, bias_sigma=0.1, x_dtype="bf16",
+               layout="contiguous", seed=0x5EED0002, layers=8),
+    "c3": dict(workload="c3: c2 paged into 64-row INT4 tiles at shuffled offsets of a 16 GB pool",
+               hidden=7168, inter=2048, g=32, sdt="bf16", sigma=0.01, E=384, shared=1, k=8,
+               mode=1, scaling=2.827, router_sigma=0.01, bias_sigma=0.1, x_dtype="bf16",
+               layout="paged", seed=0x5EED0003, layers=4),
+    "c1": dict(workload="c1: Mixtral-8x7B MoE layer decode, batch 1 (router fp32 [8,4096] softmax "
+                        "top-2; 8 INT4 experts 14336x4096, g128 fp16 scales; x fp16)",
+               hidden=4096, inter=14336, g=128, sdt="f16", sigma=0.02, E=8, shared=0, k=2,
+               mode=0, scaling=1.0, router_sigma=0.02, bias_sigma=None, x_dtype="f16",
+               layout="contiguous", seed=0x5EED0001, layers=4),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(cfg, shape) -> dict:
+    """Bytes the decode must read: touched experts' pages, router weights + bias, activation."""
+    from vib3_amd.moe import page_bytes
+    gu = 2 * page_bytes(cfg["inter"], cfg["hidden"], cfg["g"])
+    dn = page_bytes(cfg["hidden"], cfg["inter"], cfg["g"])
+    n = cfg["k"] + cfg["shared"]
+    x_bytes = cfg["hidden"] * (2 if cfg["x_dtype"] != "f32" else 4)
+    router = cfg["E"] * cfg["hidden"] * 4 + (cfg["E"] * 4 if cfg["bias_sigma"] is not None else 0)
+    h_bytes = n * cfg["inter"] * 2
+    return {
+        "router": router + x_bytes,
+        "gateup": n * gu + x_bytes + h_bytes,          # weights + x in, h out
+        "down": n * dn + h_bytes + cfg["hidden"] * 4,  # weights + h in, out
+        "layer": router + n * (gu + dn) + x_bytes + cfg["hidden"] * 4,
+    }
+
+
+def cpu_baseline(cfg, bank, w, b, x, ids, wts, budget_s: float):
+    """Time the oracle (C restatement of vib3's CPU fallback) on the same layer and token."""
+    import numpy as np
+    from oracle import oracle as O
+    threads = min(16, os.cpu_count() or 1)
+    xh = x.float().cpu().numpy()
+    wh = w.cpu().numpy()
+    bh = b.cpu().numpy() if b is not None else None
+    ids = ids.astype(np.uint16)
+    routed = {int(e): bank.expert_pages_host(int(e)) for e in ids}
+    shared = [bank.expert_pages_host(cfg["E"] + s) for s in range(cfg["shared"])]
+    sdt = O.BF16 if cfg["sdt"] == "bf16" else O.F16
+
+    def one():
+        r_ids, r_wts, _ = O.router(xh, wh, O.F32, cfg["E"], cfg["hidden"], cfg["k"], cfg["mode"],
+                                   cfg["scaling"], True, bh, nthreads=threads)
+        O.moe_layer(xh, cfg["hidden"], cfg["inter"], cfg["g"], sdt, routed, r_ids, r_wts, shared,
+                    faithful=True, nthreads=threads)
+
+    one()  # warm-up (page the copied weights in)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    med = statistics.median(times)
+    return {"value": med * 1e6, "unit": "us/layer", "cores": threads, "kind": "port",
+            "sample": f"c-oracle restatement of kernels.rs CPU fallback (router + "
+                      f"{cfg['k']}+{cfg['shared']} experts, f16 rounding points kept) on the same "
+                      f"layer/token as the GPU; median of {len(times)} reps, {threads} threads",
+            "reps": len(times)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--layers", type=int, default=0, help="layers to rotate (default per config)")
+    ap.add_argument("--tokens", type=int, default=64)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 1 GiB device copy (counter scaling for PMC runs)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build targets a single MI355X (no multi-GPU "
+              "path); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from vib3_amd import _hip, _lib, moe
+    from vib3_amd._lib import DT_BF16, DT_F16, DT_F32
+
+    cfg = dict(CONFIGS[args.config])
+    if args.layers:
+        cfg["layers"] = args.layers
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    st = stream.cuda_stream
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[cfg["x_dtype"]]
+    shape = moe.BankShape(hidden=cfg["hidden"], inter=cfg["inter"], group_size=cfg["g"],
+                          scale_dtype=DT_BF16 if cfg["sdt"] == "bf16" else DT_F16,
+                          scale_sigma=cfg["sigma"], num_experts=cfg["E"], num_shared=cfg["shared"])
+
+    t0 = time.perf_counter()
+    layers = []
+    for l in range(cfg["layers"]):
+        bank = moe.Int4ExpertBank(shape, layer=l, seed=cfg["seed"], layout=cfg["layout"],
+                                  tile_rows=64, pool_bytes=(16 << 30) if cfg["layout"] == "paged" else None,
+                                  device=dev)
+        w, b = moe.make_router(shape, l, cfg["seed"], cfg["router_sigma"], cfg["bias_sigma"],
+                               device=dev)
+        layers.append(moe.MoeInt4Layer(bank, w, b, top_k=cfg["k"], scoring_mode=cfg["mode"],
+                                       scaling_factor=cfg["scaling"], normalize=True))
+        torch.cuda.synchronize()
+        log(f"[bench] layer {l} ready ({bank.nbytes / 1e9:.2f} GB, {time.perf_counter() - t0:.1f}s)")
+    xs = [moe.make_activation(cfg["hidden"], t, cfg["seed"], dtype=tdt, device=dev)
+          for t in range(args.tokens)]
+    descs = [[ly._desc(x) for x in xs] for ly in layers]
+    lib = _lib.load()
+    launch = lib.vib3_launch_moe_int4_layer
+    L = len(layers)
+
+    def step(i: int) -> None:
+        rc = launch(descs[i % L][i % args.tokens], st)
+        if rc:
+            raise _lib.Vib3Error("vib3_launch_moe_int4_layer", rc)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = _hip.Event(), _hip.Event()
+    torch.cuda.synchronize()
+    e0.record(st)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    e1.record(st)
+    e1.synchronize()
+    torch.cuda.synchronize()
+    total_ms = e0.elapsed_ms(e1)
+    us_per_layer = total_ms * 1e3 / args.steps
+    log(f"[bench] {args.steps} steps: {us_per_layer:.2f} us/layer")
+
+    # per-stage times (separate pass: events between the three launches of each step)
+    ev = [[_hip.Event() for _ in range(4)] for _ in range(args.steps)]
+    import ctypes as C
+    for i in range(args.steps):
+        arr = (C.c_void_p * 4)(*[e.h for e in ev[i]])
+        rc = lib.vib3_launch_moe_int4_layer_timed(descs[i % L][(args.warmup + i) % args.tokens], st,
+                                                  arr)
+        if rc:
+            raise _lib.Vib3Error("vib3_launch_moe_int4_layer_timed", rc)
+    torch.cuda.synchronize()
+    stage = {"router": [], "gateup": [], "down": []}
+    for i in range(args.steps):
+        stage["router"].append(ev[i][0].elapsed_ms(ev[i][1]) * 1e3)
+        stage["gateup"].append(ev[i][1].elapsed_ms(ev[i][2]) * 1e3)
+        stage["down"].append(ev[i][2].elapsed_ms(ev[i][3]) * 1e3)
+    stage_us = {k: statistics.mean(v) for k, v in stage.items()}
+
+    nbytes = algorithmic_bytes(cfg, shape)
+    gu_gbs = nbytes["gateup"] / (stage_us["gateup"] * 1e-6) / 1e9
+    layer_gbs = nbytes["layer"] / (us_per_layer * 1e-6) / 1e9
+    expert_gbs = (nbytes["gateup"] + nbytes["down"]) / ((stage_us["gateup"] + stage_us["down"]) * 1e-6) / 1e9
+
+    copy_gbs = None
+    if True:  # achievable device copy bandwidth, reported beside the 8 TB/s peak
+        n = 1 << 30
+        src = torch.empty(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty(n, dtype=torch.uint8, device=dev)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        c0, c1 = _hip.Event(), _hip.Event()
+        c0.record(st)
+        for _ in range(10):
+            dst.copy_(src)
+        c1.record(st)
+        c1.synchronize()
+        copy_gbs = 2 * n * 10 / (c0.elapsed_ms(c1) * 1e-3) / 1e9
+        del src, dst
+
+    cpu = None
+    if not args.no_cpu:
+        ly = layers[0]
+        x = xs[0]
+        ly.launch(x)
+        torch.cuda.synchronize()
+        ids = ly.ids.cpu().numpy().view(np.uint16)[: cfg["k"]]
+        wts = ly.wts.cpu().numpy()[: cfg["k"]]
+        cpu = cpu_baseline(cfg, ly.bank, ly.router_w, ly.router_bias, x, ids, wts,
+                           args.cpu_seconds)
+        log(f"[bench] cpu baseline {cpu['value']:.0f} us/layer ({cpu['cores']} threads)")
+
+    out = {
+        "metric": "MoE layer decode us (batch 1, Kimi-K2.5 shape); expert GEMV achieved HBM GB/s"
+                  if args.config != "c1" else "MoE layer decode us (batch 1, Mixtral shape)",
+        "value": round(us_per_layer, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms / args.steps, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 weights x bf16 activations, f32 accumulate",
+        "data": "synthetic (counter-based generator; random-init weights of the named shape)",
+        "config": {"workload": cfg["workload"], "layers_rotated": L, "tokens": args.tokens,
+                   "layout": cfg["layout"], "algorithmic_bytes_per_layer": nbytes["layer"]},
+        "roofline": {"bound": "hbm", "kernel": "k_int4_rows<4,true> (fused gate/up GEMV + SwiGLU)",
+                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "algorithmic_bytes_per_launch": nbytes["gateup"],
+                     "avg_launch_us": round(stage_us["gateup"], 3)},
+        "stages_us": {k: round(v, 3) for k, v in stage_us.items()},
+        "layer_gbs": round(layer_gbs, 1),
+        "expert_gemv_gbs": round(expert_gbs, 1),
+        "copy_gbs": round(copy_gbs, 1) if copy_gbs else None,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -113,10 +113,10 @@ int vib3_launch_partial_swiglu_int4_ex(const void *input, int input_dtype, const
                                        int k, int m_slice, int group_size, int scale_dtype,
                                        void *stream);
 
-/* run_router_with_scoring_and_bias (kernels.rs:2307) on device in one launch: logits with
+/* run_router_with_scoring_and_bias (kernels.rs:2307) on device: logits with
  * hidden/weight dtypes of choice, optional f32 bias (selection only), optional normalisation.
- * workspace: at least vib3_router_workspace_bytes(num_experts) bytes, zeroed once before first
- * use (vib3_hip_zero) and left ready for the next call. scores_out may be NULL. */
+ * Two launches (logits, selection). workspace: at least vib3_router_workspace_bytes(num_experts)
+ * bytes of scratch. scores_out may be NULL. */
 size_t vib3_router_workspace_bytes(int num_experts);
 int vib3_launch_router_topk_ex(const void *hidden, int hidden_dtype, const void *router_weights,
                                int weight_dtype, const float *bias, int hidden_dim,
@@ -128,7 +128,8 @@ int vib3_launch_router_topk_ex(const void *hidden, int hidden_dtype, const void 
 /* ------------------------------------------------------------------------------------------
  * Fused MoE layer for batch-1 decode over page-indexed INT4 experts: router -> device ids and
  * weights -> page-table lookup -> fused gate/up GEMV + SwiGLU -> down GEMV with the weighted
- * sum over experts in its epilogue. Three launches, no host synchronisation.
+ * sum over experts in its epilogue. Three launches (router logits; top-k selection + gate/up;
+ * down), no host synchronisation, no atomics, deterministic.
  * Generalises vib3_launch_moe_experts_fused_gpu (cuda_ffi.rs:831, kernels.cu:5868): any number
  * of pages per matrix, INT4 instead of NVFP4, shared experts in the same launches.
  * ---------------------------------------------------------------------------------------- */
@@ -168,12 +169,18 @@ typedef struct vib3_moe_int4_layer {
     uint16_t *out_ids;    /* [top_k] or NULL */
     float *out_weights;   /* [top_k] or NULL */
     float *out_scores;    /* [num_experts] raw logits or NULL */
-    void *workspace;      /* vib3_moe_int4_workspace_bytes(), zeroed once (vib3_hip_zero) */
+    void *workspace;      /* vib3_moe_int4_workspace_bytes() bytes of scratch */
     size_t workspace_bytes;
 } vib3_moe_int4_layer;
 
 size_t vib3_moe_int4_workspace_bytes(const vib3_moe_int4_layer *layer);
 int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer *layer, void *stream);
+
+/* Same launches with hipEvent_t events[0..3] (any may be NULL) recorded on `stream` before the
+ * router, after the router, after the gate/up kernel and after the down kernel, so each stage
+ * can be timed on the stream it runs on. */
+int vib3_launch_moe_int4_layer_timed(const vib3_moe_int4_layer *layer, void *stream,
+                                     void *const *events);
 
 /* ------------------------------------------------------------------------------------------
  * Utilities

@@ -10,7 +10,8 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libvib3_hip.so")
+# VIB3_LIB may point at another build of the same ABI (e.g. an instrumented one)
+LIB_PATH = os.environ.get("VIB3_LIB") or os.path.join(HERE, "libvib3_hip.so")
 
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 ROUTER_SOFTMAX, ROUTER_SIGMOID = 0, 1
@@ -62,6 +63,7 @@ SIGNATURES = {
     "vib3_launch_router_topk_ex": (I, [P, I, P, I, P, I, I, I, I, F, I, P, P, P, P, P]),
     "vib3_moe_int4_workspace_bytes": (S, [C.POINTER(MoeInt4Layer)]),
     "vib3_launch_moe_int4_layer": (I, [C.POINTER(MoeInt4Layer), P]),
+    "vib3_launch_moe_int4_layer_timed": (I, [C.POINTER(MoeInt4Layer), P, C.POINTER(P)]),
     "vib3_hip_zero": (I, [P, S, P]),
     "vib3_synth_bytes": (I, [P, S, U64, U64, S, P]),
     "vib3_synth_normal": (I, [P, I, S, U64, U64, S, F, P]),

@@ -56,7 +56,7 @@ __global__ void k_weighted_acc(float* out, const void* e, int e_f32, float w, in
   const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
   if (i >= n) return;
   const float v = e_f32 ? ((const float*)e)[i] : f16_to_f32(((const uint16_t*)e)[i]);
-  out[i] = __fadd_rn(out[i], __fmul_rn(w, v));
+  out[i] = add_mul_rn(out[i], w, v);
 }
 
 __global__ void k_zero(uint4* p16, size_t n16, uint8_t* tail, size_t ntail) {
@@ -65,17 +65,16 @@ __global__ void k_zero(uint4* p16, size_t n16, uint8_t* tail, size_t ntail) {
   if (i < ntail) tail[i] = 0;
 }
 
-// Workspace of the fused layer: [counter | scores[E] | ids[k] | wts[k] | h[nslots][inter]].
+// Workspace of the fused layer: [scores[E] | ids[k] | wts[k] | h[nslots][inter]].
 struct LayerWs {
-  size_t counter, scores, ids, wts, h, total;
+  size_t scores, ids, wts, h, total;
 };
 
 LayerWs layer_ws(const vib3_moe_int4_layer* L) {
   LayerWs w{};
   const int nslots = L->top_k + L->num_shared;
   const size_t hsz = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? 4 : 2;
-  w.counter = 0;
-  w.scores = 256;
+  w.scores = 0;
   w.ids = round_up(w.scores + 4 * (size_t)(L->num_experts > 0 ? L->num_experts : 0), 256);
   w.wts = round_up(w.ids + 2 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
   w.h = round_up(w.wts + 4 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
@@ -214,7 +213,7 @@ int vib3_launch_partial_swiglu_int4_ex(const void* input, int input_dtype, const
 }
 
 size_t vib3_router_workspace_bytes(int num_experts) {
-  return 256 + round_up(4 * (size_t)(num_experts > 0 ? num_experts : 0), 256) + 256 + 512;
+  return round_up(4 * (size_t)(num_experts > 0 ? num_experts : 0), 256) + 256 + 256;
 }
 
 int vib3_launch_router_topk_ex(const void* hidden, int hidden_dtype, const void* router_weights,
@@ -230,19 +229,20 @@ int vib3_launch_router_topk_ex(const void* hidden, int hidden_dtype, const void*
     return VIB3_ERR_BAD_COUNT;
   if (!hidden || !router_weights || !workspace) return VIB3_ERR_BAD_POINTER;
   char* ws = (char*)workspace;
-  const size_t sc = 256, ids = sc + round_up(4 * (size_t)num_experts, 256), wts = ids + 256;
+  const size_t sc = 0, ids = round_up(4 * (size_t)num_experts, 256), wts = ids + 256;
   RouterArgs a{};
   a.x = hidden; a.x_dt = hidden_dtype; a.w = router_weights; a.w_dt = weight_dtype;
   a.bias = bias; a.D = hidden_dim; a.E = num_experts; a.top_k = top_k; a.mode = scoring_mode;
   a.scaling = scoring_mode == VIB3_ROUTER_SIGMOID ? scaling_factor : 1.0f;
   a.normalize = normalize;
-  a.counter = (unsigned*)ws;
   a.scores = scores_out ? scores_out : (float*)(ws + sc);
   a.ids = (uint16_t*)(ws + ids);
   a.wts = (float*)(ws + wts);
   a.out_ids = out_ids;
   a.out_wts = out_weights;
-  return launch_router_fused(a, S(stream));
+  const int rc = launch_router_logits(a, S(stream));
+  if (rc) return rc;
+  return launch_router_select(a, S(stream));
 }
 
 size_t vib3_moe_int4_workspace_bytes(const vib3_moe_int4_layer* L) {
@@ -250,7 +250,7 @@ size_t vib3_moe_int4_workspace_bytes(const vib3_moe_int4_layer* L) {
   return layer_ws(L).total;
 }
 
-int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
+static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, void* const* events) {
   if (!L) return VIB3_ERR_BAD_POINTER;
   if (!valid_act_dt(L->x_dtype) || !valid_scale_dt(L->scale_dtype)) return VIB3_ERR_UNSUPPORTED;
   if (L->hidden <= 0 || L->inter <= 0 || L->group_size <= 0 || L->top_k < 0 ||
@@ -273,9 +273,15 @@ int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
   if (L->workspace_bytes < w.total) return VIB3_ERR_WORKSPACE;
   char* ws = (char*)L->workspace;
   hipStream_t st = S(stream);
+  auto mark = [&](int i) {
+    if (events && events[i]) (void)hipEventRecord((hipEvent_t)events[i], st);
+  };
+  mark(0);
 
   const uint16_t* ids = (const uint16_t*)(ws + w.ids);
   const float* wts = (const float*)(ws + w.wts);
+  RouterArgs router{};
+  bool route_in_kernel = false;
   if (L->top_k > 0) {
     if (L->router_w) {
       if (!valid_act_dt(L->router_w_dtype)) return VIB3_ERR_UNSUPPORTED;
@@ -283,20 +289,24 @@ int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
         return VIB3_ERR_BAD_COUNT;
       if (L->scoring_mode != VIB3_ROUTER_SOFTMAX && L->scoring_mode != VIB3_ROUTER_SIGMOID)
         return VIB3_ERR_UNSUPPORTED;
-      RouterArgs r{};
-      r.x = L->x; r.x_dt = L->x_dtype; r.w = L->router_w; r.w_dt = L->router_w_dtype;
-      r.bias = L->router_bias; r.D = L->hidden; r.E = L->num_experts; r.top_k = L->top_k;
-      r.mode = L->scoring_mode;
-      r.scaling = L->scoring_mode == VIB3_ROUTER_SIGMOID ? L->scaling_factor : 1.0f;
-      r.normalize = L->normalize;
-      r.counter = (unsigned*)(ws + w.counter);
-      r.scores = L->out_scores ? L->out_scores : (float*)(ws + w.scores);
-      r.ids = (uint16_t*)(ws + w.ids);
-      r.wts = (float*)(ws + w.wts);
-      r.out_ids = L->out_ids;
-      r.out_wts = L->out_weights;
-      int rc = launch_router_fused(r, st);
+      router.x = L->x; router.x_dt = L->x_dtype; router.w = L->router_w;
+      router.w_dt = L->router_w_dtype; router.bias = L->router_bias; router.D = L->hidden;
+      router.E = L->num_experts; router.top_k = L->top_k; router.mode = L->scoring_mode;
+      router.scaling = L->scoring_mode == VIB3_ROUTER_SIGMOID ? L->scaling_factor : 1.0f;
+      router.normalize = L->normalize;
+      router.scores = L->out_scores ? L->out_scores : (float*)(ws + w.scores);
+      router.ids = (uint16_t*)(ws + w.ids);
+      router.wts = (float*)(ws + w.wts);
+      router.out_ids = L->out_ids;
+      router.out_wts = L->out_weights;
+      int rc = launch_router_logits(router, st);
       if (rc) return rc;
+      // small expert counts select inside the gate/up kernel; larger ones need a launch
+      route_in_kernel = L->num_experts <= kMaxExpertsInKernel && L->hidden <= 256 * 32;
+      if (!route_in_kernel) {
+        rc = launch_router_select(router, st);
+        if (rc) return rc;
+      }
     } else {
       if (!L->in_ids || !L->in_weights) return VIB3_ERR_BAD_POINTER;
       ids = L->in_ids;
@@ -304,6 +314,7 @@ int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
     }
   }
 
+  mark(1);
   const int h_dt = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? VIB3_DT_F32 : VIB3_DT_F16;
   RowsArgs a{};
   a.x = L->x; a.x_dt = L->x_dtype; a.K = L->hidden; a.M = L->inter; a.g = L->group_size;
@@ -312,8 +323,11 @@ int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
   a.top_k = L->top_k; a.max_pages = L->max_pages;
   a.rpp[0] = L->rows_per_page[0]; a.rpp[1] = L->rows_per_page[1]; a.rpp[2] = L->rows_per_page[2];
   a.out = ws + w.h; a.out_dt = h_dt; a.out_stride = (size_t)L->inter;
+  a.route = route_in_kernel;
+  a.router = router;
   int rc = launch_rows(a, true, st);
   if (rc) return rc;
+  mark(2);
 
   DownArgs d{};
   d.h = ws + w.h; d.h_dt = h_dt; d.K = L->inter; d.M = L->hidden; d.g = L->group_size;
@@ -322,7 +336,18 @@ int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
   d.max_pages = L->max_pages; d.rpp = L->rows_per_page[2];
   d.round_f16 = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? 0 : 1;
   d.out = L->out;
-  return launch_down(d, st);
+  rc = launch_down(d, st);
+  mark(3);
+  return rc;
+}
+
+int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
+  return moe_int4_layer(L, stream, nullptr);
+}
+
+int vib3_launch_moe_int4_layer_timed(const vib3_moe_int4_layer* L, void* stream,
+                                     void* const* events) {
+  return moe_int4_layer(L, stream, events);
 }
 
 }  // extern "C"

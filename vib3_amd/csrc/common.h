@@ -68,6 +68,13 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// o + w * d with the product rounded before the add (never fused into an FMA), the way the
+// reference's `*o += weight * x` compiles.
+__device__ __forceinline__ float add_mul_rn(float o, float w, float d) {
+#pragma clang fp contract(off)
+  return o + w * d;
+}
+
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
 // ------------------------------------------------------------------------- INT4 chunk dot
@@ -178,6 +185,12 @@ typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
 __device__ __forceinline__ uint4 ld_stream(const uint8_t* p) {
   const u32x4 v = __builtin_nontemporal_load((global_u32x4*)p);
   return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// 2-byte load through the global address space (pointers read from page tables are generic;
+// a flat load would also count against the LDS counter and force conservative waits).
+__device__ __forceinline__ uint16_t ld_u16(const uint16_t* p) {
+  return *(__attribute__((address_space(1))) const uint16_t*)p;
 }
 
 // ------------------------------------------------------------------------- matrix addressing

@@ -8,6 +8,28 @@
 
 namespace vib3 {
 
+// Router: logits (one workgroup per expert) and top-k selection (one wavefront, select.h).
+struct RouterArgs {
+  const void* x;
+  int x_dt;
+  const void* w;
+  int w_dt;
+  const float* bias;
+  int D, E, top_k, mode;
+  float scaling;
+  int normalize;
+  float* scores;       // [E] logits
+  uint16_t* ids;       // [top_k] selection (workspace)
+  float* wts;          // [top_k]
+  uint16_t* out_ids;   // optional copies for the caller
+  float* out_wts;
+};
+
+int launch_router_logits(const RouterArgs& a, hipStream_t s);
+int launch_router_select(const RouterArgs& a, hipStream_t s);
+
+// Experts whose selection fits the register path of select.h (8 keys per lane).
+constexpr int kMaxExpertsInKernel = 8 * 64;
 // Rows of one matrix (or of the up/gate pair) per expert slot. Slot s of a paged launch reads
 // expert ids[s] from routed_table for s < top_k and shared expert s - top_k from shared_table;
 // a flat launch (routed_table == nullptr, one slot) reads flat0 / flat1.
@@ -28,6 +50,10 @@ struct RowsArgs {
   size_t out_stride;  // elements between slots in out
   int KS;             // waves that split one row's k range (set by the launcher)
   int RPT;            // rows per team
+  // When `route` is set, every workgroup selects the top-k of router.scores in its prologue
+  // (wave 0; block 0 also publishes router.ids / router.wts) instead of reading `ids`.
+  int route;
+  RouterArgs router;
 };
 
 // Down projection of every slot for a block of RB output rows plus the weighted expert sum.
@@ -64,29 +90,6 @@ struct GenericArgs {
 int launch_rows(RowsArgs a, bool dual, hipStream_t s);
 int launch_down(DownArgs a, hipStream_t s);
 int launch_generic(GenericArgs a, bool dual, hipStream_t s);
-
-// Router: logits (one workgroup per expert) and, when fused, top-k selection by the last
-// workgroup to finish. ws_* are device buffers of the caller's workspace.
-struct RouterArgs {
-  const void* x;
-  int x_dt;
-  const void* w;
-  int w_dt;
-  const float* bias;
-  int D, E, top_k, mode;
-  float scaling;
-  int normalize;
-  float* scores;       // [E] logits (workspace or caller)
-  unsigned* counter;   // completion counter (fused only), zero between launches
-  uint16_t* ids;       // [top_k] selection (workspace)
-  float* wts;          // [top_k]
-  uint16_t* out_ids;   // optional copies for the caller
-  float* out_wts;
-};
-
-int launch_router_fused(const RouterArgs& a, hipStream_t s);
-int launch_router_logits(const RouterArgs& a, hipStream_t s);
-int launch_router_select(const RouterArgs& a, hipStream_t s);
 
 constexpr int kMaxExperts = 4096;
 

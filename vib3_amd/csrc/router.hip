@@ -3,15 +3,15 @@
 // Logits: one 256-thread workgroup per expert row; each thread reads 8 consecutive weights per
 // step with 16-byte loads (f32 rows: two loads), the wave reduces with DPP, four wave sums are
 // combined in a fixed order. Selection: one wavefront holds the scores in LDS and picks the
-// top-k by k rounds of a wave-wide (key desc, index asc) arg-max — stable-sort order of the
-// reference (kernels.rs:2370, :2416) for any expert count up to 4096, unlike the power-of-two
-// bitonic sort of kernels.cu:4011. The fused launch lets the last workgroup to finish its
-// logit (completion counter, release/acquire fences) run the selection, so routing costs one
-// launch and no host synchronisation.
+// top-k by k rounds of a wave-wide (key desc, index asc) arg-max (select.h) — stable-sort order
+// of the reference (kernels.rs:2370, :2416) for any expert count up to 4096, unlike the
+// power-of-two bitonic sort of kernels.cu:4011. Inside the fused MoE layer the selection runs
+// in the prologue of the gate/up kernel instead of a launch of its own.
 #include <math.h>
 
 #include "common.h"
 #include "kernels.h"
+#include "select.h"
 
 namespace vib3 {
 
@@ -55,7 +55,8 @@ __device__ __forceinline__ void load8_stream(const void* p, int dt, size_t i, fl
 }
 
 // Dot product of x with router row e, computed by the whole 256-thread workgroup; the result is
-// valid in thread 0.
+// valid in every thread. Each thread owns 8-element groups tid, tid+256, ...; the loads of four
+// groups are issued before any arithmetic so a row's 28 KB is in flight at once.
 __device__ float router_row_dot(const RouterArgs& a, int e) {
   __shared__ float red[4];
   const int tid = (int)threadIdx.x;
@@ -66,14 +67,23 @@ __device__ float router_row_dot(const RouterArgs& a, int e) {
   const bool vec = (D % 8 == 0) && (((uintptr_t)row & 15) == 0) &&
                    ((((uintptr_t)a.x) & 15) == 0);
   if (vec) {
-    const size_t n8 = D / 8;
-#pragma unroll 4
-    for (size_t i = (size_t)tid; i < n8; i += 256) {
-      float w[8], x[8];
-      load8_stream(row, a.w_dt, i * 8, w);
-      load8_act(a.x, a.x_dt, i * 8, x);
+    const int n8 = (int)(D / 8);
+    for (int base = 0; base < n8; base += 4 * 256) {
+      float w[4][8], x[4][8];
 #pragma unroll
-      for (int j = 0; j < 8; j++) acc = __builtin_fmaf(x[j], w[j], acc);
+      for (int u = 0; u < 4; u++) {
+        const int i = base + u * 256 + tid;
+        const int ic = i < n8 ? i : 0;
+        load8_stream(row, a.w_dt, (size_t)ic * 8, w[u]);
+        load8_act(a.x, a.x_dt, (size_t)ic * 8, x[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        if (base + u * 256 + tid < n8) {
+#pragma unroll
+          for (int j = 0; j < 8; j++) acc = __builtin_fmaf(x[u][j], w[u][j], acc);
+        }
+      }
     }
   } else {
     for (size_t d = (size_t)tid; d < D; d += 256)
@@ -85,102 +95,17 @@ __device__ float router_row_dot(const RouterArgs& a, int e) {
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// Top-k selection by wave 0 of the calling workgroup (64 threads participate).
-__device__ void router_select_wave(const RouterArgs& a, const float* scores) {
-  __shared__ float key[kMaxExperts];
-  __shared__ float val[kMaxExperts];
-  __shared__ unsigned char taken[kMaxExperts];
-  __shared__ int sel[64];
-  const int lane = lane_id();
-  const int E = a.E;
-  for (int e = lane; e < E; e += kWave) {
-    const float s = scores[e];
-    float v = s, k = s;
-    if (a.mode == VIB3_ROUTER_SIGMOID) {
-      v = 1.0f / (1.0f + expf(-s));
-      k = a.bias ? v + a.bias[e] : v;
-    }
-    if (k != k) k = -__builtin_huge_valf();  // NaN ranks last
-    key[e] = k;
-    val[e] = v;
-    taken[e] = 0;
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  for (int j = 0; j < a.top_k; j++) {
-    float bk = -__builtin_huge_valf();
-    int bi = 0x7fffffff;
-    for (int e = lane; e < E; e += kWave) {
-      if (taken[e]) continue;
-      const float k = key[e];
-      if (k > bk || (k == bk && e < bi)) { bk = k; bi = e; }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ok = __shfl_xor(bk, off);
-      const int oi = __shfl_xor(bi, off);
-      if (ok > bk || (ok == bk && oi < bi)) { bk = ok; bi = oi; }
-    }
-    if (lane == (bi & 63)) taken[bi] = 1;
-    if (lane == 0) sel[j] = bi;
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-  }
-  if (lane != 0) return;
-  // Weights (kernels.rs:2368-2387 softmax, :2389-2436 sigmoid), sequential like the reference.
-  float w[64];
-  if (a.mode == VIB3_ROUTER_SOFTMAX) {
-    float mx = -__builtin_huge_valf();
-    for (int j = 0; j < a.top_k; j++) mx = fmaxf(mx, val[sel[j]]);
-    float sum = 0.0f;
-    for (int j = 0; j < a.top_k; j++) sum += expf(val[sel[j]] - mx);
-    for (int j = 0; j < a.top_k; j++) w[j] = expf(val[sel[j]] - mx) / sum;
-  } else {
-    for (int j = 0; j < a.top_k; j++) w[j] = val[sel[j]];
-    if (a.normalize) {
-      float total = 0.0f;
-      for (int j = 0; j < a.top_k; j++) total += w[j];
-      if (total > 1e-20f)
-        for (int j = 0; j < a.top_k; j++) w[j] /= total;
-    }
-    for (int j = 0; j < a.top_k; j++) w[j] *= a.scaling;
-  }
-  for (int j = 0; j < a.top_k; j++) {
-    a.ids[j] = (uint16_t)sel[j];
-    a.wts[j] = w[j];
-    if (a.out_ids) a.out_ids[j] = (uint16_t)sel[j];
-    if (a.out_wts) a.out_wts[j] = w[j];
-  }
-}
-
 __global__ __launch_bounds__(256) void k_router_logits(RouterArgs a) {
   const float s = router_row_dot(a, (int)blockIdx.x);
   if (threadIdx.x == 0) a.scores[blockIdx.x] = s;
 }
 
-__global__ __launch_bounds__(64) void k_router_select(RouterArgs a) { router_select_wave(a, a.scores); }
-
-__global__ __launch_bounds__(256) void k_router_fused(RouterArgs a) {
-  __shared__ int is_last;
-  const float s = router_row_dot(a, (int)blockIdx.x);
-  if (threadIdx.x == 0) {
-    a.scores[blockIdx.x] = s;
-    __threadfence();  // release the logit before counting this workgroup as done
-    const unsigned prev = atomicAdd(a.counter, 1u);
-    is_last = prev == gridDim.x - 1;
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();  // acquire every other workgroup's logit
-  if (threadIdx.x < 64) {
-    router_select_wave(a, a.scores);
-    if (threadIdx.x == 0) atomicExch(a.counter, 0u);  // ready for the next launch
-  }
-}
-
-int launch_router_fused(const RouterArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_router_fused, dim3((unsigned)a.E), dim3(256), 0, s, a);
-  VIB3_RETURN_LAUNCH();
+template <bool REGS>
+__global__ __launch_bounds__(64) void k_router_select(RouterArgs a) {
+  __shared__ int sel[64];
+  __shared__ float wts[64];
+  if (REGS) select_topk_regs<8>(a, a.scores, sel, wts, true);
+  else select_topk_lds(a, a.scores, sel, wts, true);
 }
 
 int launch_router_logits(const RouterArgs& a, hipStream_t s) {
@@ -189,7 +114,8 @@ int launch_router_logits(const RouterArgs& a, hipStream_t s) {
 }
 
 int launch_router_select(const RouterArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_router_select, dim3(1), dim3(64), 0, s, a);
+  if (a.E <= 8 * kWave) hipLaunchKernelGGL(k_router_select<true>, dim3(1), dim3(64), 0, s, a);
+  else hipLaunchKernelGGL(k_router_select<false>, dim3(1), dim3(64), 0, s, a);
   VIB3_RETURN_LAUNCH();
 }
 
