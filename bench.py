@@ -113,8 +113,8 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--copy-probe", action="store_true",
-                    help="also run a plain 1 GiB device copy (counter scaling for PMC runs)")
+    ap.add_argument("--given-ids", action="store_true",
+                    help="skip the router: experts come from preset device id lists (diagnostic)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -155,7 +155,16 @@ def main() -> int:
         log(f"[bench] layer {l} ready ({bank.nbytes / 1e9:.2f} GB, {time.perf_counter() - t0:.1f}s)")
     xs = [moe.make_activation(cfg["hidden"], t, cfg["seed"], dtype=tdt, device=dev)
           for t in range(args.tokens)]
-    descs = [[ly._desc(x) for x in xs] for ly in layers]
+    if args.given_ids:
+        rng = np.random.default_rng(cfg["seed"])
+        gid = [torch.from_numpy(rng.choice(cfg["E"], cfg["k"], replace=False).astype(np.int16)).to(dev)
+               for _ in range(args.tokens)]
+        gw = torch.full((cfg["k"],), 1.0 / cfg["k"], dtype=torch.float32, device=dev)
+        for ly in layers:
+            ly.router_w = None
+        descs = [[ly._desc(x, gid[t], gw) for t, x in enumerate(xs)] for ly in layers]
+    else:
+        descs = [[ly._desc(x) for x in xs] for ly in layers]
     lib = _lib.load()
     launch = lib.vib3_launch_moe_int4_layer
     L = len(layers)
@@ -219,7 +228,7 @@ def main() -> int:
         del src, dst
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not args.given_ids:
         ly = layers[0]
         x = xs[0]
         ly.launch(x)

@@ -31,8 +31,8 @@ int int4_flat(const void* x, int x_dt, const void* d0, const void* s0, const voi
   if (fast) {
     RowsArgs a{};
     a.x = x; a.x_dt = x_dt; a.K = k; a.M = m; a.g = g; a.sdt = sdt; a.nslots = 1;
-    a.flat0 = MatRef{nullptr, (const uint8_t*)d0, (const uint16_t*)s0, 0, m};
-    a.flat1 = dual ? MatRef{nullptr, (const uint8_t*)d1, (const uint16_t*)s1, 0, m} : a.flat0;
+    a.flat0 = MatRef{nullptr, (const uint8_t*)d0, (const uint16_t*)s0, 0, m, 0};
+    a.flat1 = dual ? MatRef{nullptr, (const uint8_t*)d1, (const uint16_t*)s1, 0, m, 0} : a.flat0;
     a.out = out; a.out_dt = out_dt; a.out_stride = 0;
     return launch_rows(a, dual, st);
   }
@@ -259,6 +259,7 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, void* cons
   const int nslots = L->top_k + L->num_shared;
   if (nslots <= 0 || nslots > 16 || L->top_k > 64) return VIB3_ERR_BAD_COUNT;
   if (L->hidden % 32 || L->inter % 32) return VIB3_ERR_UNSUPPORTED;
+  if (L->hidden >= 65536 || L->inter >= 65536) return VIB3_ERR_UNSUPPORTED;  // page_magic range
   for (int s = 0; s < 3; s++)
     if (L->rows_per_page[s] <= 0) return VIB3_ERR_BAD_COUNT;
   if ((L->rows_per_page[0] + 0LL) * L->max_pages < L->inter ||
@@ -321,7 +322,10 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, void* cons
   a.sdt = L->scale_dtype; a.nslots = nslots;
   a.routed_table = L->page_table; a.shared_table = L->shared_page_table; a.ids = ids;
   a.top_k = L->top_k; a.max_pages = L->max_pages;
-  a.rpp[0] = L->rows_per_page[0]; a.rpp[1] = L->rows_per_page[1]; a.rpp[2] = L->rows_per_page[2];
+  for (int q = 0; q < 3; q++) {
+    a.rpp[q] = L->rows_per_page[q];
+    a.magic[q] = page_magic(L->rows_per_page[q]);
+  }
   a.out = ws + w.h; a.out_dt = h_dt; a.out_stride = (size_t)L->inter;
   a.route = route_in_kernel;
   a.router = router;
@@ -334,6 +338,7 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, void* cons
   d.sdt = L->scale_dtype; d.nslots = nslots; d.routed_table = L->page_table;
   d.shared_table = L->shared_page_table; d.ids = ids; d.wts = wts; d.top_k = L->top_k;
   d.max_pages = L->max_pages; d.rpp = L->rows_per_page[2];
+  d.magic = page_magic(L->rows_per_page[2]);
   d.round_f16 = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? 0 : 1;
   d.out = L->out;
   rc = launch_down(d, st);

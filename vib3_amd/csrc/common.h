@@ -193,6 +193,23 @@ __device__ __forceinline__ uint16_t ld_u16(const uint16_t* p) {
   return *(__attribute__((address_space(1))) const uint16_t*)p;
 }
 
+// Page-table entry through the constant address space: with a wave-uniform address this is a
+// scalar load (s_load), so waiting for it never involves the vector memory counter. Page tables
+// are read-only while a kernel runs.
+__device__ __forceinline__ uint64_t ld_table(const uint64_t* p) {
+  return *(const __attribute__((address_space(4))) uint64_t*)p;
+}
+
+// A pointer every lane holds the same value of (e.g. read from LDS), moved to SGPRs so that
+// loads through it are scalar and their waits do not involve the vector memory counter.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  return (T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 // ------------------------------------------------------------------------- matrix addressing
 //
 // An INT4 matrix is either flat (data rows then scale rows at explicit pointers) or a list of
@@ -200,20 +217,27 @@ __device__ __forceinline__ uint16_t ld_u16(const uint16_t* p) {
 // (the last page may be short). row() resolves one row with a single table read.
 
 struct MatRef {
-  const uint64_t* table;  // paged when non-null: table[page]
-  const uint8_t* data;    // flat
-  const uint16_t* scales; // flat
+  const uint64_t* table;  // paged: table[page] = page address
+  const uint8_t* data;    // flat: data rows
+  const uint16_t* scales; // flat: scale rows
   int rpp;                // rows per page (paged)
   int rows;               // rows of the whole matrix
+  uint64_t magic;         // ceil(2^32 / rpp): page = (row * magic) >> 32 (exact for rows < 2^16)
 };
 
+__host__ __device__ inline uint64_t page_magic(int rpp) {
+  return ((1ull << 32) + (uint64_t)rpp - 1) / (uint64_t)rpp;
+}
+
+// Row r of a matrix: data and scale-row pointers. Paged: one table read, no branch, no divide.
+template <bool PAGED>
 __device__ __forceinline__ void mat_row(const MatRef& m, int r, int pk, int ng, const uint8_t*& d,
                                         const uint16_t*& s) {
-  if (m.table) {
-    int p = r / m.rpp;
-    int rr = r - p * m.rpp;
-    int rows_here = min(m.rpp, m.rows - p * m.rpp);
-    const uint8_t* base = (const uint8_t*)m.table[p];
+  if (PAGED) {
+    const int p = (int)(((uint64_t)(uint32_t)r * m.magic) >> 32);
+    const int rr = r - p * m.rpp;
+    const int rows_here = min(m.rpp, m.rows - p * m.rpp);
+    const uint8_t* base = (const uint8_t*)ld_table(m.table + p);
     d = base + (size_t)rr * pk;
     s = (const uint16_t*)(base + (size_t)rows_here * pk) + (size_t)rr * ng;
   } else {

@@ -33,22 +33,27 @@ struct RowBatch {
   uint16_t q0[U][NCH], q1[U][NCH];
 };
 
-template <int NCH, bool DUAL, int U>
+template <bool PAGED, int NCH, bool DUAL, int U>
 __device__ __forceinline__ void issue(RowBatch<NCH, DUAL, U>& b, const MatRef& m0, const MatRef& m1,
                                       const int (&ra)[U], const int (&cidx)[NCH],
-                                      const int (&gidx)[NCH], int pk, int ng, int cpr) {
+                                      const int (&gidx)[NCH], int pk, int ng, int cpr,
+                                      const void* dummy = nullptr) {
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const uint8_t *d0, *d1 = nullptr;
     const uint16_t *s0, *s1 = nullptr;
-    mat_row(m0, ra[u], pk, ng, d0, s0);
-    if (DUAL) mat_row(m1, ra[u], pk, ng, d1, s1);
+    mat_row<PAGED>(m0, ra[u], pk, ng, d0, s0);
+    if (DUAL) mat_row<PAGED>(m1, ra[u], pk, ng, d1, s1);
+    if (dummy) {  // a batch past the end: the same loads from a small cached buffer, no branch
+      d0 = d1 = (const uint8_t*)dummy;
+      s0 = s1 = (const uint16_t*)dummy;
+    }
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
       // lanes past the last chunk re-read it (no divergent branch around the loads); their
       // activation chunk is zero, so they add nothing
       const int c = min(cidx[j], cpr - 1);
-      const size_t off = (size_t)c * 16;
+      const uint32_t off = (uint32_t)c * 16u;  // 32-bit lane offset on a uniform row base
       b.w0[u][j] = ld_stream(d0 + off);
       b.q0[u][j] = ld_u16(s0 + gidx[j]);
       if (DUAL) {
@@ -83,13 +88,13 @@ __device__ __forceinline__ void reduce(const RowBatch<NCH, DUAL, U>& b, const XC
   }
 }
 
-template <int NCH, bool DUAL, bool SPLIT, int U>
+template <bool PAGED, int NCH, bool DUAL, bool SPLIT, int U>
 __device__ __forceinline__ void dot_rows(const MatRef& m0, const MatRef& m1, const int (&ra)[U],
                                          const XChunk (&xh)[NCH], const XChunk (&xl)[NCH],
                                          const int (&cidx)[NCH], const int (&gidx)[NCH], int pk,
                                          int ng, int cpr, int sdt, float (&t0)[U], float (&t1)[U]) {
   RowBatch<NCH, DUAL, U> b;
-  issue<NCH, DUAL, U>(b, m0, m1, ra, cidx, gidx, pk, ng, cpr);
+  issue<PAGED, NCH, DUAL, U>(b, m0, m1, ra, cidx, gidx, pk, ng, cpr);
   reduce<NCH, DUAL, SPLIT, U>(b, xh, xl, cidx, cpr, sdt, t0, t1);
 }
 
@@ -127,11 +132,11 @@ __device__ __forceinline__ void load_x(const void* x, int x_dt, int cpr, const i
 // are shared experts s - top_k; flat launches use flat0 / flat1.
 __device__ __forceinline__ MatRef slot_matrix(const RowsArgs& a, int slot, int expert, int seg,
                                               int which) {
-  if (!a.routed_table) return which == 0 ? a.flat0 : a.flat1;
+  if (!a.routed_table) return which == 0 ? a.flat0 : a.flat1;  // flat launch
   const uint64_t* t;
   if (slot < a.top_k) t = a.routed_table + ((size_t)expert * 3 + seg) * a.max_pages;
   else t = a.shared_table + ((size_t)(slot - a.top_k) * 3 + seg) * a.max_pages;
-  return MatRef{t, nullptr, nullptr, a.rpp[seg], a.M};
+  return MatRef{t, nullptr, nullptr, a.rpp[seg], a.M, a.magic[seg]};
 }
 
 __device__ __forceinline__ float rows_epilogue(bool dual, float up, float gate) {
@@ -150,7 +155,7 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, size_t o, float v) 
 // stride over them (grid sized to the resident capacity), so all CUs stay busy to the end.
 // KS > 1: the KS waves of a team split one row's k range and combine through LDS.
 
-template <int NCH, bool DUAL, bool SPLIT>
+template <int NCH, bool DUAL, bool SPLIT, bool PAGED>
 __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform (SGPR)
@@ -158,64 +163,158 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   XChunk xh[NCH], xl[NCH];
   int cidx[NCH], gidx[NCH];
 
-  if (a.KS == 1) {
-    // Items are (slot, row), shared-expert slots first; waves stride over them. Two load
-    // buffers alternate so the next item's 16-byte loads are in flight while the current one
-    // is reduced (no register copies of in-flight loads, which would force a wait).
-    __shared__ int s_sel[64];
-    __shared__ float s_wts[64];
-    chunk_index<NCH>(0, a.g, cpr, cidx, gidx);
-    const int items = a.nslots * a.M;
-    const int stride = (int)gridDim.x * 4;
-    int it = (int)blockIdx.x * 4 + wave;
-    auto slot_of = [&](int item) {
-      const int q = item / a.M;
-      return a.nslots > a.top_k ? (q + a.top_k) % a.nslots : q;
-    };
-    auto expert_of = [&](int slot) {
-      if (slot >= a.top_k || !a.routed_table) return 0;
-      return a.route ? __builtin_amdgcn_readfirstlane(s_sel[slot]) : (int)a.ids[slot];
-    };
-    RowBatch<NCH, DUAL, 1> A, B;
-    auto start = [&](RowBatch<NCH, DUAL, 1>& buf, int item) {
-      const int slot = slot_of(item);
-      const int e = expert_of(slot);
-      const MatRef m0 = slot_matrix(a, slot, e, 0, 0);
-      const MatRef m1 = DUAL ? slot_matrix(a, slot, e, 1, 1) : m0;
-      const int ra[1] = {item - (item / a.M) * a.M};
-      issue<NCH, DUAL, 1>(buf, m0, m1, ra, cidx, gidx, pk, ng, cpr);
-    };
-    auto finish = [&](const RowBatch<NCH, DUAL, 1>& buf, int item) {
-      float t0[1], t1[1];
-      reduce<NCH, DUAL, SPLIT, 1>(buf, xh, xl, cidx, cpr, a.sdt, t0, t1);
-      const int slot = slot_of(item);
-      if (lane == 0)
-        store_out(a, (size_t)slot * a.out_stride + (item - (item / a.M) * a.M),
-                  rows_epilogue(DUAL, t0[0], t1[0]));
-    };
-    // a shared-expert row needs no routing: start its loads before the selection
-    const bool early = it < items && slot_of(it) >= a.top_k;
-    if (early) start(A, it);
-    if (a.route) {
-      if (wave == 0) select_topk_regs<8>(a.router, a.router.scores, s_sel, s_wts, blockIdx.x == 0);
-      __syncthreads();
+  // Items are (slot, row), shared-expert slots first; waves stride over them. Three load
+  // buffers rotate so the next two items' 16-byte loads are in flight while the current one
+  // is reduced (no register copies of in-flight loads, which would force a wait).
+  __shared__ int s_sel[64];
+  __shared__ float s_wts[64];
+  // per slot: page-table row of each matrix (resolved once; a 16-bit id load in the loop
+  // would be a vector load whose wait drains all prefetched weight loads)
+  __shared__ const uint64_t* s_tab[16][2];
+  chunk_index<NCH>(0, a.g, cpr, cidx, gidx);
+  const int items = a.nslots * a.M;
+  const int stride = (int)gridDim.x * 4;
+  const int M = a.M, nslots = a.nslots, top_k = a.top_k;
+  const int rpp0 = a.rpp[0], rpp1 = a.rpp[1];
+  const uint64_t magic0 = a.magic[0], magic1 = a.magic[1];
+  // item = q * M + row; q maps to a slot with the shared experts first
+  const int it0 = (int)blockIdx.x * 4 + wave;
+  auto slot_of = [&](int q) {  // q < nslots; shared slots (>= top_k) come first
+    if (nslots == top_k) return q;
+    const int v = q + top_k;
+    return v >= nslots ? v - nslots : v;
+  };
+  auto shared_table_of = [&](int slot, int which) {
+    return a.shared_table + ((size_t)(slot - top_k) * 3 + which) * a.max_pages;
+  };
+  // Lane k of this wave holds its k-th item's row and page-table rows (filled after routing);
+  // the loop fetches them with v_readlane: no memory access, so no wait can drain the
+  // prefetched weight loads.
+  int my_row = 0;
+  uint64_t my_t0 = 0, my_t1 = 0;
+  RowBatch<NCH, DUAL, 1> A, B, C;
+  // start() is issued unconditionally: a batch past the last item reads the activation
+  // vector instead (all wave-uniform selects). A branch around the loads would leave the
+  // compiler's wait counting unsure how many loads are in flight, and it would then wait for
+  // all of them.
+  auto start = [&](RowBatch<NCH, DUAL, 1>& buf, int k, bool direct, int item) {
+    const bool past = item >= items;
+    MatRef m0, m1;
+    int row;
+    if (PAGED) {
+      const uint64_t* t0;
+      const uint64_t* t1;
+      if (direct) {  // first item, shared expert: straight from the kernel arguments
+        const int q = item / M;
+        row = item - q * M;
+        t0 = shared_table_of(slot_of(q), 0);
+        t1 = shared_table_of(slot_of(q), 1);
+      } else {
+        k &= kWave - 1;  // k may run two past the last item; any lane holds a valid row
+        row = __builtin_amdgcn_readlane(my_row, k);
+        t0 = (const uint64_t*)(uintptr_t)(
+            ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(my_t0 >> 32), k) << 32) |
+            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)my_t0, k));
+        t1 = (const uint64_t*)(uintptr_t)(
+            ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(my_t1 >> 32), k) << 32) |
+            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)my_t1, k));
+      }
+      m0 = MatRef{t0, nullptr, nullptr, rpp0, M, magic0};
+      m1 = DUAL ? MatRef{t1, nullptr, nullptr, rpp1, M, magic1} : m0;
+    } else {
+      row = min(item, items - 1);  // flat launches have one slot
+      m0 = a.flat0;
+      m1 = a.flat1;
     }
-    if (it >= items) return;
-    if (!early) start(A, it);
-    load_x<NCH, SPLIT>(a.x, a.x_dt, cpr, cidx, xh, xl);
-    for (;;) {
-      const int i1 = it + stride;
-      if (i1 < items) start(B, i1);
-      finish(A, it);
-      if (i1 >= items) break;
-      const int i2 = i1 + stride;
-      if (i2 < items) start(A, i2);
-      finish(B, i1);
-      if (i2 >= items) break;
-      it = i2;
-    }
-    return;
+    const int ra[1] = {row};
+    issue<PAGED, NCH, DUAL, 1>(buf, m0, m1, ra, cidx, gidx, pk, ng, cpr,
+                               past ? a.x : nullptr);
+    // keep the scheduler from sinking these loads below the previous batch's arithmetic
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Results stay in lanes (lane k holds this wave's k-th item; the launcher keeps k < 64)
+  // and are stored after the loop: a store inside it would share the load counter and make
+  // the waits drain the prefetched loads.
+  float res = 0.f;
+  int kres = 0;
+  auto finish = [&](const RowBatch<NCH, DUAL, 1>& buf) {
+    float t0[1], t1[1];
+    reduce<NCH, DUAL, SPLIT, 1>(buf, xh, xl, cidx, cpr, a.sdt, t0, t1);
+    const float v = rows_epilogue(DUAL, t0[0], t1[0]);
+    if (lane == kres) res = v;
+    kres++;
+  };
+  const bool have = it0 < items;
+  if (PAGED && wave == 0 && lane < nslots && lane >= top_k) {
+    s_tab[lane][0] = shared_table_of(lane, 0);
+    s_tab[lane][1] = shared_table_of(lane, 1);
   }
+  // a shared-expert row needs no routing: start its loads before the selection
+  const bool early = have && PAGED && slot_of(it0 / M) >= top_k;
+  if (early) start(A, 0, true, it0);
+  if (PAGED && top_k > 0 && wave == 0) {
+    if (a.route) {
+      select_topk_regs<8>(a.router, a.router.scores, s_sel, s_wts, blockIdx.x == 0);
+    } else if (lane < top_k) {
+      s_sel[lane] = a.ids[lane];
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    if (lane < top_k) {
+      const uint64_t* rt = a.routed_table + (size_t)s_sel[lane] * 3 * a.max_pages;
+      s_tab[lane][0] = rt;
+      s_tab[lane][1] = rt + a.max_pages;
+    }
+  }
+  __syncthreads();
+  if (!have) return;
+  if (PAGED) {
+    // lane k <- this wave's k-th item (lanes past the end keep a valid page-table row)
+    const int item = min(it0 + lane * stride, items - 1);
+    {
+      const int q = item / M;
+      my_row = item - q * M;
+      const int slot = slot_of(q);
+      my_t0 = (uint64_t)(uintptr_t)s_tab[slot][0];
+      my_t1 = (uint64_t)(uintptr_t)s_tab[slot][1];
+    }
+  }
+  if (!early) start(A, 0, false, it0);
+  // three buffers: while item i is reduced, items i+1 and i+2 are loading
+  int it = it0, k = 0;
+  start(B, 1, false, it + stride);
+  load_x<NCH, SPLIT>(a.x, a.x_dt, cpr, cidx, xh, xl);
+  for (;;) {
+    start(C, k + 2, false, it + 2 * stride);
+    finish(A);
+    if (it + stride >= items) break;
+    it += stride;
+    k++;
+    start(A, k + 2, false, it + 2 * stride);
+    finish(B);
+    if (it + stride >= items) break;
+    it += stride;
+    k++;
+    start(B, k + 2, false, it + 2 * stride);
+    finish(C);
+    if (it + stride >= items) break;
+    it += stride;
+    k++;
+  }
+  if (lane < kres) {
+    const int item = it0 + lane * stride;
+    const int q = item / M;
+    store_out(a, (size_t)slot_of(q) * a.out_stride + (item - q * M), res);
+  }
+}
+
+template <int NCH, bool DUAL, bool SPLIT, bool PAGED>
+__global__ __launch_bounds__(256) void k_int4_rows_ksplit(RowsArgs a) {
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform (SGPR)
+  const int pk = a.K / 2, ng = (a.K + a.g - 1) / a.g, cpr = a.K / 32;
+  XChunk xh[NCH], xl[NCH];
+  int cidx[NCH], gidx[NCH];
 
   const int ks = wave % a.KS;
   const int team = wave / a.KS;
@@ -223,7 +322,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   const int slot = (int)blockIdx.y;
   const int r0 = ((int)blockIdx.x * teams + team) * a.RPT;
   const int nrows = max(0, min(a.RPT, a.M - r0));
-  const int e = (a.routed_table && slot < a.top_k) ? (int)a.ids[slot] : 0;
+  const int e = (PAGED && slot < a.top_k) ? (int)a.ids[slot] : 0;
   const MatRef m0 = slot_matrix(a, slot, e, 0, 0);
   const MatRef m1 = DUAL ? slot_matrix(a, slot, e, 1, 1) : m0;
   chunk_index<NCH>(ks, a.g, cpr, cidx, gidx);
@@ -232,7 +331,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   for (int i = 0; i < nrows; i += 2) {
     const int ra[2] = {r0 + i, i + 1 < nrows ? r0 + i + 1 : r0 + i};
     float t0[2], t1[2];
-    dot_rows<NCH, DUAL, SPLIT, 2>(m0, m1, ra, xh, xl, cidx, gidx, pk, ng, cpr, a.sdt, t0, t1);
+    dot_rows<PAGED, NCH, DUAL, SPLIT, 2>(m0, m1, ra, xh, xl, cidx, gidx, pk, ng, cpr, a.sdt, t0, t1);
     if (lane == i) { res0 = t0[0]; res1 = t1[0]; }
     if (lane == i + 1) { res0 = t0[1]; res1 = t1[1]; }
   }
@@ -254,58 +353,126 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
 
 // ------------------------------------------------------------------------- k_down_combine
 //
-// One workgroup = nslots * KS waves (one wave per expert slot and k part); it strides over
-// blocks of RB output rows. Each wave computes its slot's rows, the per-row results meet in
-// LDS, and wave 0 forms sum_s w_s * f16(d_s) in slot order (router order, then shared).
+// Down projection of every expert slot for blocks of RB output rows, plus the weighted expert
+// sum. A row is handled by 16 lanes (4 rows per wave instruction): lane `sub` of a 16-lane group
+// owns chunks sub + 16 j (j < 4) of the wave's k range, so one 16-byte load per lane per j
+// reads four 256-byte row segments, and a row's sum needs only 4 DPP steps inside the group
+// (no cross-row readlanes). One workgroup = nslots * KS waves (slot, k part); per-row sums meet
+// in LDS and wave 0 forms sum_s w_s * f16(d_s) in slot order (router order, then shared).
 
-template <int NCH, bool SPLIT>
-__global__ __launch_bounds__(1024) void k_down_combine(DownArgs a) {
+constexpr int kDownJ = 4;        // chunks per lane per row
+constexpr int kDownRows = 4;     // rows per wave instruction (64 lanes / 16)
+constexpr int kDownSpan = 16 * kDownJ;  // chunks of one k part
+
+// Sum over each 16-lane row of the wave; every lane gets its row's total.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  return v;
+}
+
+template <int U>
+struct DownBatch {
+  uint4 w[U][kDownJ];
+  uint16_t q[U][kDownJ];
+};
+
+// WIDE: up to 16 waves per workgroup (VGPRs capped at 128: one 4-row group per batch);
+// otherwise up to 10 waves with two 4-row groups (8 KB per wave) per batch.
+template <bool SPLIT, bool WIDE>
+__global__ __launch_bounds__(WIDE ? 1024 : 640) void k_down_combine(DownArgs a) {
+  constexpr int U = 1;  // one 4-row group per batch (two batches in flight)
   const int lane = lane_id();
-  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform (SGPR)
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int slot = wave / a.KS;
-  const int ks = wave % a.KS;
+  const int ks = wave - slot * a.KS;
+  const int grp = lane >> 4, sub = lane & 15;
   const int pk = a.K / 2, ng = (a.K + a.g - 1) / a.g, cpr = a.K / 32;
 
+  // the slot's expert id is a 16-bit (vector) load: make the table row wave-uniform once
+  const int expert = slot < a.top_k ? __builtin_amdgcn_readfirstlane((int)a.ids[slot]) : 0;
   const uint64_t* t = slot < a.top_k
-                          ? a.routed_table + ((size_t)a.ids[slot] * 3 + 2) * a.max_pages
+                          ? a.routed_table + ((size_t)expert * 3 + 2) * a.max_pages
                           : a.shared_table + ((size_t)(slot - a.top_k) * 3 + 2) * a.max_pages;
-  const MatRef m{t, nullptr, nullptr, a.rpp, a.M};
-  XChunk xh[NCH], xl[NCH];
-  int cidx[NCH], gidx[NCH];
-  chunk_index<NCH>(ks, a.g, cpr, cidx, gidx);
+  const MatRef m{uniform_ptr(t), nullptr, nullptr, a.rpp, a.M, a.magic};
+
+  // this lane's chunks (clamped for the loads; chunks past the end get a zero activation)
+  int cidx[kDownJ], cld[kDownJ], gidx[kDownJ];
+#pragma unroll
+  for (int j = 0; j < kDownJ; j++) {
+    cidx[j] = ks * kDownSpan + sub + 16 * j;
+    cld[j] = min(cidx[j], cpr - 1);
+    gidx[j] = (cld[j] * 32) / a.g;
+  }
   const char* hbase = (const char*)a.h + (size_t)slot * a.K * (a.h_dt == VIB3_DT_F32 ? 4 : 2);
 
-  constexpr int U = NCH == 1 ? 4 : 2;  // rows per batch (keeps NCH=2 within 128 VGPRs)
-  // This workgroup's items: blocks b = blockIdx.x + n * gridDim.x, each in ceil(RB / U)
-  // batches of U rows (the last block's surplus rows repeat its last row and are dropped).
-  // Two load buffers alternate; the first batch is issued before h is even read.
   __shared__ float part[16][kWave];
   const int blocks = (a.M + a.RB - 1) / a.RB;
   if ((int)blockIdx.x >= blocks) return;
-  const int ipb = (a.RB + U - 1) / U;
+  constexpr int RPB = kDownRows * U;            // rows per batch
+  const int ipb = (a.RB + RPB - 1) / RPB;       // batches per block
   const int my_blocks = (blocks - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
   const int n = my_blocks * ipb;
-  RowBatch<NCH, false, U> A, B;
-  float res = 0.f;
-  auto start = [&](RowBatch<NCH, false, U>& buf, int k) {
-    const int bb = (int)blockIdx.x + (k / ipb) * (int)gridDim.x;
-    const int r0 = bb * a.RB, nr = min(a.RB, a.M - r0), i0 = (k % ipb) * U;
-    int ra[U];
-#pragma unroll
-    for (int u = 0; u < U; u++) ra[u] = r0 + min(i0 + u, nr - 1);
-    issue<NCH, false, U>(buf, m, m, ra, cidx, gidx, pk, ng, cpr);
+  struct Pos { int bb, i0; };
+  auto advance = [&](Pos p) {
+    p.i0 += RPB;
+    if (p.i0 >= ipb * RPB) { p.i0 = 0; p.bb += (int)gridDim.x; }
+    return p;
   };
-  auto finish = [&](const RowBatch<NCH, false, U>& buf, int k) {
-    const int bb = (int)blockIdx.x + (k / ipb) * (int)gridDim.x;
-    const int r0 = bb * a.RB, nr = min(a.RB, a.M - r0), i0 = (k % ipb) * U;
-    float t0[U], t1[U];
-    reduce<NCH, false, SPLIT, U>(buf, xh, xl, cidx, cpr, a.sdt, t0, t1);
+  // start() runs unconditionally (see k_int4_rows): a batch past the end resolves row M - 1
+  // and then reads the activation buffer instead
+  auto start = [&](DownBatch<U>& b, Pos p, bool past) {
+    const int r0 = p.bb * a.RB, nr = min(a.RB, a.M - r0);
 #pragma unroll
-    for (int u = 0; u < U; u++)
-      if (lane == i0 + u) res = t0[u];
-    if (k % ipb == ipb - 1) {
+    for (int u = 0; u < U; u++) {
+      // the four rows of a batch are wave-uniform values: resolve each with a scalar table
+      // read, then every 16-lane group picks its own
+      const uint8_t* d = nullptr;
+      const uint16_t* sc = nullptr;
+#pragma unroll
+      for (int q = 0; q < kDownRows; q++) {
+        const int r = r0 + min(p.i0 + u * kDownRows + q, nr - 1);
+        const uint8_t* dq;
+        const uint16_t* sq;
+        mat_row<true>(m, r, pk, ng, dq, sq);
+        if (grp == q) { d = dq; sc = sq; }
+      }
+      if (past) {
+        d = (const uint8_t*)hbase;
+        sc = (const uint16_t*)hbase;
+      }
+#pragma unroll
+      for (int j = 0; j < kDownJ; j++) {
+        b.w[u][j] = ld_stream(d + (size_t)cld[j] * 16);
+        b.q[u][j] = ld_u16(sc + gidx[j]);
+      }
+    }
+    // keep the scheduler from sinking these loads below the previous batch's arithmetic
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // router weights: lane s holds slot s's (read once; a load at each block's combine would
+  // wait for every weight load in flight)
+  const float my_w = lane < a.top_k ? a.wts[lane] : 0.f;
+  XChunk xh[kDownJ], xl[kDownJ];
+  auto finish = [&](const DownBatch<U>& b, Pos p) {
+    const int r0 = p.bb * a.RB, nr = min(a.RB, a.M - r0);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < kDownJ; j++) {
+        float pj = chunk_dot(b.w[u][j], xh[j]);
+        if (SPLIT) pj += chunk_dot(b.w[u][j], xl[j]);
+        acc = __builtin_fmaf(pj, decode_scale(b.q[u][j], a.sdt), acc);
+      }
+      const float sum = row16_sum(acc) * kTwo24;
+      const int i = p.i0 + u * kDownRows + grp;
+      if (sub == 0 && i < kWave) part[wave][i] = sum;
+    }
+    if (p.i0 + RPB >= ipb * RPB) {
       // block complete: combine the slots' rows
-      part[wave][lane] = res;
       __syncthreads();
       if (wave == 0 && lane < nr) {
         // weighted_accumulate_f32 over the slots in router order, then the shared experts
@@ -315,24 +482,40 @@ __global__ __launch_bounds__(1024) void k_down_combine(DownArgs a) {
           float d = 0.0f;
           for (int q = 0; q < a.KS; q++) d += part[s * a.KS + q][lane];
           if (a.round_f16) d = (float)(half_t)d;
-          const float w = s < a.top_k ? a.wts[s] : 1.0f;
+          const float w = s < a.top_k ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), s)) : 1.0f;
           o = add_mul_rn(o, w, d);
         }
         a.out[r0 + lane] = o;
       }
       __syncthreads();
-      res = 0.f;
     }
   };
-  start(A, 0);
-  load_x<NCH, SPLIT>(hbase, a.h_dt, cpr, cidx, xh, xl);
+  DownBatch<U> A, B;
+  Pos q0{(int)blockIdx.x, 0};
+  Pos q1 = advance(q0);
+  start(A, q0, false);
+  // activations: the 4 chunks of h this lane multiplies, loaded after the first weights
+#pragma unroll
+  for (int j = 0; j < kDownJ; j++) {
+    if (cidx[j] < cpr) {
+      float xv[32];
+      load_chunk_act(hbase, a.h_dt, cidx[j], xv);
+      make_chunk(xv, xh[j], xl[j]);
+      if (!SPLIT) zero_chunk(xl[j]);
+    } else {
+      zero_chunk(xh[j]);
+      zero_chunk(xl[j]);
+    }
+  }
   for (int k = 0;; k += 2) {
-    if (k + 1 < n) start(B, k + 1);
-    finish(A, k);
+    start(B, q1, k + 1 >= n);
+    finish(A, q0);
     if (k + 1 >= n) break;
-    if (k + 2 < n) start(A, k + 2);
-    finish(B, k + 1);
+    q0 = advance(q1);
+    start(A, q0, k + 2 >= n);
+    finish(B, q1);
     if (k + 2 >= n) break;
+    q1 = advance(q0);
   }
 }
 
@@ -417,23 +600,32 @@ static int env_int(const char* name, int dflt) {
   return v && atoi(v) > 0 ? atoi(v) : dflt;
 }
 
-template <int N, bool D, bool S>
-static void launch_rows_t(RowsArgs& a, hipStream_t s) {
-  auto k = k_int4_rows<N, D, S>;
+template <int N, bool D, bool S, bool P>
+static void launch_rows_p(RowsArgs& a, hipStream_t s) {
   if (a.KS == 1) {
+    auto k = k_int4_rows<N, D, S, P>;
     const int items = a.nslots * a.M;
     const int want = (items + 3) / 4;
     int cap = resident_blocks(k, 256);
     const int per_cu = env_int("VIB3_ROWS_BLOCKS_PER_CU", 0);
     if (per_cu > 0 && per_cu * device_cus() < cap) cap = per_cu * device_cus();
+    const int floor_blocks = (items + 4 * kWave - 1) / (4 * kWave);  // <= 64 items per wave
+    if (cap < floor_blocks) cap = floor_blocks;
     hipLaunchKernelGGL(k, dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0, s, a);
   } else {
+    auto k = k_int4_rows_ksplit<N, D, S, P>;
     const int teams = 4 / a.KS;
     dim3 grid((unsigned)((a.M + teams * a.RPT - 1) / (teams * a.RPT)), (unsigned)a.nslots);
     hipLaunchKernelGGL(k, grid, dim3(256), 0, s, a);
   }
 }
 
+
+template <int N, bool D, bool S>
+static void launch_rows_t(RowsArgs& a, hipStream_t s) {
+  if (!a.routed_table) return launch_rows_p<N, D, S, false>(a, s);
+  return launch_rows_p<N, D, S, true>(a, s);
+}
 int launch_rows(RowsArgs a, bool dual, hipStream_t s) {
   const int cpr = a.K / 32;
   int nch = 1, ks = 1;
@@ -460,16 +652,17 @@ int launch_rows(RowsArgs a, bool dual, hipStream_t s) {
   VIB3_RETURN_LAUNCH();
 }
 
-template <int N, bool S>
+template <bool S, bool W>
 static void launch_down_t(DownArgs& a, hipStream_t s) {
-  auto k = k_down_combine<N, S>;
+  auto k = k_down_combine<S, W>;
   const int block = a.nslots * a.KS * kWave;
   int cap = resident_blocks(k, block);
   const int per_cu = env_int("VIB3_DOWN_BLOCKS_PER_CU", 0);
   if (per_cu > 0 && per_cu * device_cus() < cap) cap = per_cu * device_cus();
-  // rows per block: spread the rows evenly over the resident workgroups, multiple of 4
+  // rows per block: spread the rows evenly over the resident workgroups, a multiple of the
+  // 8-row batch, at most 64 (one LDS column per row)
   int rb = (a.M + cap - 1) / cap;
-  rb = (rb + 3) / 4 * 4;  // a multiple of both batch sizes (4 and 2)
+  rb = (rb + 7) / 8 * 8;  // multiple of both batch heights (4 and 8)
   if (rb > kWave) rb = kWave;
   a.RB = rb;
   const int blocks = (a.M + rb - 1) / rb;
@@ -479,19 +672,17 @@ static void launch_down_t(DownArgs& a, hipStream_t s) {
 
 int launch_down(DownArgs a, hipStream_t s) {
   const int cpr = a.K / 32;
-  // NCH <= 2 keeps a 1024-thread workgroup within 128 VGPRs per lane.
-  const int nch = cpr <= kWave ? 1 : 2;
-  const int ks = (cpr + nch * kWave - 1) / (nch * kWave);
+  const int ks = (cpr + kDownSpan - 1) / kDownSpan;
   if (a.nslots * ks > 16) return VIB3_ERR_UNSUPPORTED;
   a.KS = ks;
   if (a.M <= 0) return 0;
-  const bool split = a.h_dt == VIB3_DT_F32;
-  if (nch == 1) {
-    if (split) launch_down_t<1, true>(a, s);
-    else launch_down_t<1, false>(a, s);
+  const bool wide = a.nslots * ks > 10;
+  if (a.h_dt == VIB3_DT_F32) {
+    if (wide) launch_down_t<true, true>(a, s);
+    else launch_down_t<true, false>(a, s);
   } else {
-    if (split) launch_down_t<2, true>(a, s);
-    else launch_down_t<2, false>(a, s);
+    if (wide) launch_down_t<false, true>(a, s);
+    else launch_down_t<false, false>(a, s);
   }
   VIB3_RETURN_LAUNCH();
 }

@@ -44,6 +44,7 @@ struct RowsArgs {
   int top_k;
   int max_pages;
   int rpp[3];
+  uint64_t magic[3];  // page_magic(rpp[s])
   MatRef flat0, flat1;
   void* out;
   int out_dt;
@@ -69,6 +70,7 @@ struct DownArgs {
   int top_k;
   int max_pages;
   int rpp;  // rows per page of the down segment
+  uint64_t magic;  // page_magic(rpp)
   int KS;
   int RB;
   int round_f16;
