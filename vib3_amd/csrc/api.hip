@@ -304,6 +304,7 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, void* cons
       if (rc) return rc;
       // small expert counts select inside the gate/up kernel; larger ones need a launch
       route_in_kernel = L->num_experts <= kMaxExpertsInKernel && L->hidden <= 256 * 32;
+      if (const char* v = getenv("VIB3_ROUTE_IN_KERNEL")) route_in_kernel &= atoi(v) != 0;
       if (!route_in_kernel) {
         rc = launch_router_select(router, st);
         if (rc) return rc;

@@ -155,6 +155,11 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, size_t o, float v) 
 // stride over them (grid sized to the resident capacity), so all CUs stay busy to the end.
 // KS > 1: the KS waves of a team split one row's k range and combine through LDS.
 
+#ifndef VIB3_ROWS_BUFFERS
+#define VIB3_ROWS_BUFFERS 2  // load buffers per wave (build-time tuning knob)
+#endif
+constexpr int kRowsBuffers = VIB3_ROWS_BUFFERS;
+
 template <int NCH, bool DUAL, bool SPLIT, bool PAGED>
 __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   const int lane = lane_id();
@@ -192,7 +197,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // prefetched weight loads.
   int my_row = 0;
   uint64_t my_t0 = 0, my_t1 = 0;
-  RowBatch<NCH, DUAL, 1> A, B, C;
+  RowBatch<NCH, DUAL, 1> buf[kRowsBuffers];
   // start() is issued unconditionally: a batch past the last item reads the activation
   // vector instead (all wave-uniform selects). A branch around the loads would leave the
   // compiler's wait counting unsure how many loads are in flight, and it would then wait for
@@ -251,10 +256,10 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   }
   // a shared-expert row needs no routing: start its loads before the selection
   const bool early = have && PAGED && slot_of(it0 / M) >= top_k;
-  if (early) start(A, 0, true, it0);
+  if (early) start(buf[0], 0, true, it0);
   if (PAGED && top_k > 0 && wave == 0) {
     if (a.route) {
-      select_topk_regs<8>(a.router, a.router.scores, s_sel, s_wts, blockIdx.x == 0);
+      select_topk_small(a.router, a.router.scores, s_sel, s_wts, blockIdx.x == 0);
     } else if (lane < top_k) {
       s_sel[lane] = a.ids[lane];
     }
@@ -279,27 +284,23 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
       my_t1 = (uint64_t)(uintptr_t)s_tab[slot][1];
     }
   }
-  if (!early) start(A, 0, false, it0);
-  // three buffers: while item i is reduced, items i+1 and i+2 are loading
-  int it = it0, k = 0;
-  start(B, 1, false, it + stride);
+  if (!early) start(buf[0], 0, false, it0);
+  // NB buffers in a ring: while item i is reduced, items i+1 .. i+NB-1 are loading
+  for (int b = 1; b + 1 < kRowsBuffers; b++) start(buf[b], b, false, it0 + b * stride);
   load_x<NCH, SPLIT>(a.x, a.x_dt, cpr, cidx, xh, xl);
-  for (;;) {
-    start(C, k + 2, false, it + 2 * stride);
-    finish(A);
-    if (it + stride >= items) break;
-    it += stride;
-    k++;
-    start(A, k + 2, false, it + 2 * stride);
-    finish(B);
-    if (it + stride >= items) break;
-    it += stride;
-    k++;
-    start(B, k + 2, false, it + 2 * stride);
-    finish(C);
-    if (it + stride >= items) break;
-    it += stride;
-    k++;
+  for (int k = 0;; k += kRowsBuffers) {
+    bool done = false;
+#pragma unroll
+    for (int b = 0; b < kRowsBuffers; b++) {
+      const int ahead = k + b + kRowsBuffers - 1;
+      start(buf[(b + kRowsBuffers - 1) % kRowsBuffers], ahead, false, it0 + ahead * stride);
+      finish(buf[b]);
+      if (it0 + (k + b + 1) * stride >= items) {
+        done = true;
+        break;
+      }
+    }
+    if (done) break;
   }
   if (lane < kres) {
     const int item = it0 + lane * stride;
@@ -519,6 +520,161 @@ __global__ __launch_bounds__(WIDE ? 1024 : 640) void k_down_combine(DownArgs a) 
   }
 }
 
+// ------------------------------------------------------------------------- k_down_rows
+//
+// Down projection + weighted combine with the activations of every slot staged once per
+// workgroup in LDS, already in chunk_dot's pair layout (so a batch costs no conversion work).
+// A wave owns a group of 4 output rows (16 lanes per row, J chunks per lane) and walks the
+// slots in router order, so the combine o = o + w_s * d_s happens in registers in the
+// reference's order: no cross-wave reduction, no barrier in the loop. f16 intermediates and
+// k <= 64 * 32 only; other shapes use k_down_combine.
+
+template <int J>
+struct DownRowsBatch {
+  uint4 w[J];
+  uint16_t q[J];
+};
+
+template <int J, int NB>
+__global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
+  extern __shared__ uint4 lds[];
+  constexpr int CP = 16 * J;  // chunks per slot in LDS, zero past the last chunk
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int grp = lane >> 4, sub = lane & 15;
+  const int cpr = a.K / 32, pk = a.K / 2, ng = (a.K + a.g - 1) / a.g;
+  const int ns = a.nslots, top_k = a.top_k;
+  uint4* xq = lds;                                      // [ns][4][CP] pair words
+  float* xsum = (float*)(lds + (size_t)ns * 4 * CP);    // [ns][CP] offset term
+
+  // lane s < nslots holds slot s's page-table row (down segment) and router weight
+  uint64_t my_t = 0;
+  float my_w = 1.0f;
+  if (lane < ns) {
+    const uint64_t* t =
+        lane < top_k ? a.routed_table + ((size_t)a.ids[lane] * 3 + 2) * a.max_pages
+                     : a.shared_table + ((size_t)(lane - top_k) * 3 + 2) * a.max_pages;
+    my_t = (uint64_t)(uintptr_t)t;
+    if (lane < top_k) my_w = a.wts[lane];
+  }
+  int cld[J], gidx[J];
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    cld[j] = min(sub + 16 * j, cpr - 1);
+    gidx[j] = (cld[j] * 32) / a.g;
+  }
+
+  const int G = (a.M + 3) / 4;  // row groups
+  const int g0 = (int)blockIdx.x * 4 + wave;
+  const int gstride = (int)gridDim.x * 4;
+  const int ngr = g0 < G ? (G - 1 - g0) / gstride + 1 : 0;
+  const int n = ngr * ns;  // batches of this wave: (group, slot), slots innermost
+  struct Pos { int g, s; };
+  auto advance = [&](Pos p) {
+    if (++p.s == ns) { p.s = 0; p.g += gstride; }
+    return p;
+  };
+  auto start = [&](DownRowsBatch<J>& b, Pos p, bool past) {
+    const uint64_t tv =
+        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(my_t >> 32), p.s) << 32) |
+        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)my_t, p.s);
+    const MatRef m{(const uint64_t*)(uintptr_t)tv, nullptr, nullptr, a.rpp, a.M, a.magic};
+    const uint8_t* d = nullptr;
+    const uint16_t* sc = nullptr;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {  // the four rows are wave-uniform: scalar table reads
+      const int r = min(4 * p.g + q, a.M - 1);
+      const uint8_t* dq;
+      const uint16_t* sq;
+      mat_row<true>(m, r, pk, ng, dq, sq);
+      if (grp == q) { d = dq; sc = sq; }
+    }
+    if (past) {  // a batch past the end reads the (cached) intermediate instead
+      d = (const uint8_t*)a.h;
+      sc = (const uint16_t*)a.h;
+    }
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      b.w[j] = ld_stream(d + (uint32_t)cld[j] * 16u);
+      b.q[j] = ld_u16(sc + gidx[j]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  float o = 0.0f;
+  auto finish = [&](const DownRowsBatch<J>& b, Pos p) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int c = sub + 16 * j;
+      const uint4* xp = xq + (size_t)p.s * 4 * CP + c;
+      XChunk x;
+      const uint4 va = xp[0], vb = xp[CP], vc = xp[2 * CP], vd = xp[3 * CP];
+      x.a[0] = as_h2(va.x); x.a[1] = as_h2(va.y); x.a[2] = as_h2(va.z); x.a[3] = as_h2(va.w);
+      x.b[0] = as_h2(vb.x); x.b[1] = as_h2(vb.y); x.b[2] = as_h2(vb.z); x.b[3] = as_h2(vb.w);
+      x.c[0] = as_h2(vc.x); x.c[1] = as_h2(vc.y); x.c[2] = as_h2(vc.z); x.c[3] = as_h2(vc.w);
+      x.d[0] = as_h2(vd.x); x.d[1] = as_h2(vd.y); x.d[2] = as_h2(vd.z); x.d[3] = as_h2(vd.w);
+      x.xs8 = xsum[p.s * CP + c];
+      acc = __builtin_fmaf(chunk_dot(b.w[j], x), decode_scale(b.q[j], a.sdt), acc);
+    }
+    float dsum = row16_sum(acc) * kTwo24;
+    if (a.round_f16) dsum = (float)(half_t)dsum;
+    const float w = p.s < top_k ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), p.s))
+                                : 1.0f;
+    o = add_mul_rn(o, w, dsum);  // weighted_accumulate_f32 in slot order (engine.rs:5262-5302)
+    if (p.s == ns - 1) {
+      const int r = 4 * p.g + grp;
+      if (sub == 0 && r < a.M) a.out[r] = o;
+      o = 0.0f;
+    }
+  };
+
+  // NB load buffers in a ring: while batch i is reduced, batches i+1 .. i+NB-1 are loading
+  DownRowsBatch<J> buf[NB];
+  Pos pos[NB];
+  pos[0] = Pos{g0, 0};
+#pragma unroll
+  for (int b = 1; b < NB; b++) pos[b] = advance(pos[b - 1]);
+  if (n > 0) {  // the first batches load while the activations are staged
+#pragma unroll
+    for (int b = 0; b + 1 < NB; b++) start(buf[b], pos[b], b >= n);
+  }
+  const char* hb = (const char*)a.h;
+  for (int i = (int)threadIdx.x; i < ns * CP; i += (int)blockDim.x) {
+    const int sl = i / CP, c = i - sl * CP;
+    XChunk hi, lo;
+    if (c < cpr) {
+      float xv[32];
+      load_chunk_act(hb + (size_t)sl * a.K * 2, VIB3_DT_F16, c, xv);
+      make_chunk(xv, hi, lo);
+    } else {
+      zero_chunk(hi);
+    }
+    uint4* xp = xq + (size_t)sl * 4 * CP + c;
+    auto pack = [](const h2 (&v)[4]) {
+      return make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                        __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
+    };
+    xp[0] = pack(hi.a);
+    xp[CP] = pack(hi.b);
+    xp[2 * CP] = pack(hi.c);
+    xp[3 * CP] = pack(hi.d);
+    xsum[sl * CP + c] = hi.xs8;
+  }
+  __syncthreads();
+  if (n == 0) return;
+  for (int k = 0;; k += NB) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      // refill the buffer consumed last with batch k + b + NB - 1
+      const int nb = (b + NB - 1) % NB;
+      pos[nb] = advance(pos[(nb + NB - 1) % NB]);
+      start(buf[nb], pos[nb], k + b + NB - 1 >= n);
+      finish(buf[b], pos[b]);
+      if (k + b + 1 >= n) return;
+    }
+  }
+}
+
 // ------------------------------------------------------------------------- k_int4_generic
 
 template <bool DUAL>
@@ -670,8 +826,34 @@ static void launch_down_t(DownArgs& a, hipStream_t s) {
                      s, a);
 }
 
+#ifndef VIB3_DOWN_ROWS_BUFFERS
+#define VIB3_DOWN_ROWS_BUFFERS 2  // load buffers per wave (build-time tuning knob)
+#endif
+constexpr int kDownRowsBuffers = VIB3_DOWN_ROWS_BUFFERS;
+
+// LDS bytes of k_down_rows: per slot, 16 * J chunks of 4 pair words and one offset term.
+static size_t down_rows_lds(int nslots, int J) { return (size_t)nslots * 16 * J * (64 + 4); }
+
+template <int J>
+static void launch_down_rows_t(DownArgs& a, hipStream_t s) {
+  const int groups = (a.M + 3) / 4;
+  const int blocks = (groups + 3) / 4;
+  hipLaunchKernelGGL((k_down_rows<J, kDownRowsBuffers>), dim3((unsigned)blocks), dim3(256),
+                     (unsigned)down_rows_lds(a.nslots, J), s, a);
+}
+
 int launch_down(DownArgs a, hipStream_t s) {
   const int cpr = a.K / 32;
+  if (a.M <= 0) return 0;
+  // staged-activation kernel for f16 intermediates of up to 64 chunks per row
+  const int J = cpr <= 16 ? 1 : cpr <= 32 ? 2 : cpr <= 64 ? 4 : 0;
+  if (a.h_dt == VIB3_DT_F16 && J && down_rows_lds(a.nslots, J) <= 64 * 1024 &&
+      env_int("VIB3_DOWN_COMBINE", 0) == 0) {
+    if (J == 1) launch_down_rows_t<1>(a, s);
+    else if (J == 2) launch_down_rows_t<2>(a, s);
+    else launch_down_rows_t<4>(a, s);
+    VIB3_RETURN_LAUNCH();
+  }
   const int ks = (cpr + kDownSpan - 1) / kDownSpan;
   if (a.nslots * ks > 16) return VIB3_ERR_UNSUPPORTED;
   a.KS = ks;

@@ -104,7 +104,7 @@ template <bool REGS>
 __global__ __launch_bounds__(64) void k_router_select(RouterArgs a) {
   __shared__ int sel[64];
   __shared__ float wts[64];
-  if (REGS) select_topk_regs<8>(a, a.scores, sel, wts, true);
+  if (REGS) select_topk_small(a, a.scores, sel, wts, true);
   else select_topk_lds(a, a.scores, sel, wts, true);
 }
 

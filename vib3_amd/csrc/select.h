@@ -49,43 +49,83 @@ __device__ __forceinline__ void selection_key(const RouterArgs& a, float s, floa
   if (key != key) key = -__builtin_huge_valf();  // NaN ranks last
 }
 
-// Weights of the selected experts (kernels.rs:2368-2387 softmax, :2389-2436 sigmoid), computed
-// sequentially by lane 0 from the selected values; selv[j] is overwritten by the weight.
-__device__ inline void router_weights_lane0(const RouterArgs& a, const int* sel, float* selv,
-                                            bool publish) {
-  float mx = -__builtin_huge_valf(), sum = 0.0f, total = 0.0f;
+// Weights of the selected experts (kernels.rs:2368-2387 softmax, :2389-2436 sigmoid) by the
+// whole wave: lane j < top_k handles pick j. Sums run sequentially in pick order (the
+// reference's order) through readlane; the per-pick exp and divisions run in parallel.
+// sel[j] / selv[j] hold the picks and their values; selv[j] is overwritten by the weight.
+__device__ inline void router_weights_wave(const RouterArgs& a, const int* sel, float* selv,
+                                           bool publish) {
+  const int lane = lane_id();
+  const bool mine = lane < a.top_k;
+  const float v = mine ? selv[lane] : 0.0f;
+  const auto rl = [](float x, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+  };
+  float w;
   if (a.mode == VIB3_ROUTER_SOFTMAX) {
-    for (int j = 0; j < a.top_k; j++) mx = fmaxf(mx, selv[j]);
-    for (int j = 0; j < a.top_k; j++) sum += expf(selv[j] - mx);
-  } else if (a.normalize) {
-    for (int j = 0; j < a.top_k; j++) total += selv[j];
-  }
-  for (int j = 0; j < a.top_k; j++) {  // in place: each weight depends only on its own value
-    float w;
-    if (a.mode == VIB3_ROUTER_SOFTMAX) {
-      w = expf(selv[j] - mx) / sum;
-    } else {
-      w = selv[j];
-      if (a.normalize && total > 1e-20f) w /= total;
-      w *= a.scaling;
+    float mx = -__builtin_huge_valf();
+    for (int j = 0; j < a.top_k; j++) mx = fmaxf(mx, rl(v, j));
+    const float e = expf(v - mx);
+    float sum = 0.0f;
+    for (int j = 0; j < a.top_k; j++) sum += rl(e, j);
+    w = e / sum;
+  } else {
+    w = v;
+    if (a.normalize) {
+      float total = 0.0f;
+      for (int j = 0; j < a.top_k; j++) total += rl(v, j);
+      if (total > 1e-20f) w = v / total;
     }
-    selv[j] = w;
+    w *= a.scaling;
+  }
+  if (mine) {
+    selv[lane] = w;
     if (publish) {
-      a.ids[j] = (uint16_t)sel[j];
-      a.wts[j] = w;
-      if (a.out_ids) a.out_ids[j] = (uint16_t)sel[j];
-      if (a.out_wts) a.out_wts[j] = w;
+      const int id = sel[lane];
+      a.ids[lane] = (uint16_t)id;
+      a.wts[lane] = w;
+      if (a.out_ids) a.out_ids[lane] = (uint16_t)id;
+      if (a.out_wts) a.out_wts[lane] = w;
     }
   }
 }
 
-// Top-k by the calling wave (all 64 lanes). Keys live in registers: lane l owns experts
-// l, l+64, ...; each round is a local arg-max over R registers and one wave arg-max.
+// Minimum of an int over the wave (wave-uniform result).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+  v = min(v, dpp_i<0xB1>(v));
+  v = min(v, dpp_i<0x4E>(v));
+  v = min(v, dpp_i<0x141>(v));
+  v = min(v, dpp_i<0x140>(v));
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  const auto rl = [](float x, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+  };
+  return fmaxf(fmaxf(rl(v, 0), rl(v, 16)), fmaxf(rl(v, 32), rl(v, 48)));
+}
+
+// Top-k by the calling wave (all 64 lanes active). Lane l owns experts l, l+64, ... (R keys);
+// each lane first sorts its keys by (key desc, index asc), so the lane heads hold every lane's
+// best remaining candidate. A round is then branch-free: the wave maximum of the heads, a
+// ballot for the lanes that hold it (the lowest index wins a tie), and the winning lane pops
+// its head. The order of the picks is the order of a stable descending sort.
 template <int R>
 __device__ inline void select_topk_regs(const RouterArgs& a, const float* scores, int* sel,
                                         float* selv, bool publish) {
   const int lane = lane_id();
+  constexpr int kNone = 0x7fffffff;
   float key[R], val[R], sc[R], bs[R];
+  int idx[R];
   const float* bp = a.bias ? a.bias : scores;
 #pragma unroll
   for (int r = 0; r < R; r++) {  // all loads first: one round trip, not R
@@ -98,30 +138,60 @@ __device__ inline void select_topk_regs(const RouterArgs& a, const float* scores
     const int e = lane + r * kWave;
     selection_key(a, sc[r], a.bias ? bs[r] : 0.0f, key[r], val[r]);
     if (e >= a.E) key[r] = -__builtin_huge_valf();
+    idx[r] = e < a.E ? e : kNone;
   }
-  unsigned taken = 0;  // bit r: expert lane + 64r already selected
+  // insertion network: R(R-1)/2 compare-exchanges, all lanes in parallel
+#pragma unroll
+  for (int i = 1; i < R; i++) {
+#pragma unroll
+    for (int j = i; j > 0; j--) {
+      const bool sw = key[j] > key[j - 1] || (key[j] == key[j - 1] && idx[j] < idx[j - 1]);
+      const float k0 = key[j - 1], v0 = val[j - 1];
+      const int i0 = idx[j - 1];
+      key[j - 1] = sw ? key[j] : k0;
+      val[j - 1] = sw ? val[j] : v0;
+      idx[j - 1] = sw ? idx[j] : i0;
+      key[j] = sw ? k0 : key[j];
+      val[j] = sw ? v0 : val[j];
+      idx[j] = sw ? i0 : idx[j];
+    }
+  }
   for (int j = 0; j < a.top_k; j++) {
-    float bk = -__builtin_huge_valf();
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      const int e = lane + r * kWave;
-      if (e < a.E && !(taken >> r & 1u)) better(bk, bi, key[r], e);
+    const float m = wave_max_f(key[0]);
+    const bool at_max = key[0] == m;
+    const uint64_t holders = __ballot(at_max);
+    int win;
+    if (__popcll(holders) == 1) {
+      win = __builtin_amdgcn_readlane(idx[0], __ffsll((unsigned long long)holders) - 1);
+    } else {  // a tie: the lowest index wins (wave-uniform branch)
+      win = wave_min_i(at_max ? idx[0] : kNone);
     }
-    const int win = wave_argmax(bk, bi);
-    if ((win & (kWave - 1)) == lane) {
-#pragma unroll
-      for (int r = 0; r < R; r++)
-        if (r == (win >> 6)) selv[j] = val[r];
-      taken |= 1u << (win >> 6);
-    }
+    const bool pop = (win & (kWave - 1)) == lane;
+    if (pop) selv[j] = val[0];
     if (lane == 0) sel[j] = win;
+#pragma unroll
+    for (int r = 0; r + 1 < R; r++) {
+      key[r] = pop ? key[r + 1] : key[r];
+      val[r] = pop ? val[r + 1] : val[r];
+      idx[r] = pop ? idx[r + 1] : idx[r];
+    }
+    key[R - 1] = pop ? -__builtin_huge_valf() : key[R - 1];
+    idx[R - 1] = pop ? kNone : idx[R - 1];
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
-  if (lane == 0) router_weights_lane0(a, sel, selv, publish);
+  router_weights_wave(a, sel, selv, publish);
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
+}
+
+// Register selection for up to 8 * 64 experts, with the register count matched to E.
+__device__ inline void select_topk_small(const RouterArgs& a, const float* scores, int* sel,
+                                         float* selv, bool publish) {
+  if (a.E <= 2 * kWave) select_topk_regs<2>(a, scores, sel, selv, publish);
+  else if (a.E <= 4 * kWave) select_topk_regs<4>(a, scores, sel, selv, publish);
+  else if (a.E <= 6 * kWave) select_topk_regs<6>(a, scores, sel, selv, publish);
+  else select_topk_regs<8>(a, scores, sel, selv, publish);
 }
 
 // Same selection for up to kMaxExperts experts with the keys in LDS.
@@ -149,7 +219,7 @@ __device__ inline void select_topk_lds(const RouterArgs& a, const float* scores,
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
-  if (lane == 0) router_weights_lane0(a, sel, selv, publish);
+  router_weights_wave(a, sel, selv, publish);
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
 }
