@@ -189,22 +189,22 @@ def main() -> int:
     us_per_layer = total_ms * 1e3 / args.steps
     log(f"[bench] {args.steps} steps: {us_per_layer:.2f} us/layer")
 
-    # per-stage times (separate pass: events between the three launches of each step)
-    ev = [[_hip.Event() for _ in range(4)] for _ in range(args.steps)]
-    import ctypes as C
-    for i in range(args.steps):
-        arr = (C.c_void_p * 4)(*[e.h for e in ev[i]])
-        rc = lib.vib3_launch_moe_int4_layer_timed(descs[i % L][(args.warmup + i) % args.tokens], st,
-                                                  arr)
-        if rc:
-            raise _lib.Vib3Error("vib3_launch_moe_int4_layer_timed", rc)
-    torch.cuda.synchronize()
-    stage = {"router": [], "gateup": [], "down": []}
-    for i in range(args.steps):
-        stage["router"].append(ev[i][0].elapsed_ms(ev[i][1]) * 1e3)
-        stage["gateup"].append(ev[i][1].elapsed_ms(ev[i][2]) * 1e3)
-        stage["down"].append(ev[i][2].elapsed_ms(ev[i][3]) * 1e3)
-    stage_us = {k: statistics.mean(v) for k, v in stage.items()}
+    # per-stage times: each stage's launches alone, back to back over the same rotation of
+    # layers and tokens (a stage reads what the full-layer launches above left in its workspace)
+    stage_us = {}
+    for j, name in enumerate(("router", "gateup", "down")):
+        if name == "router" and args.given_ids:
+            continue
+        s0, s1 = _hip.Event(), _hip.Event()
+        s0.record(st)
+        for i in range(args.steps):
+            rc = lib.vib3_launch_moe_int4_layer_stage(descs[i % L][(args.warmup + i) % args.tokens],
+                                                      j, st)
+            if rc:
+                raise _lib.Vib3Error("vib3_launch_moe_int4_layer_stage", rc)
+        s1.record(st)
+        s1.synchronize()
+        stage_us[name] = s0.elapsed_ms(s1) * 1e3 / args.steps
 
     nbytes = algorithmic_bytes(cfg, shape)
     gu_gbs = nbytes["gateup"] / (stage_us["gateup"] * 1e-6) / 1e9
@@ -226,6 +226,14 @@ def main() -> int:
         c1.synchronize()
         copy_gbs = 2 * n * 10 / (c0.elapsed_ms(c1) * 1e-3) / 1e9
         del src, dst
+
+    # HBM traffic per launch of the roofline kernel, from the committed rocprofv3 PMC summary
+    # (FETCH_SIZE + WRITE_SIZE, each scaled by what the counter reads for a 1 GiB copy)
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
+    if os.path.exists(tpath) and not args.given_ids:
+        with open(tpath) as f:
+            traffic = json.load(f)["kernels"].get("k_int4_rows", {}).get("hbm_bytes")
 
     cpu = None
     if not args.no_cpu and not args.given_ids:
@@ -258,7 +266,8 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": "k_int4_rows<4,true> (fused gate/up GEMV + SwiGLU)",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": traffic,
+                     "traffic_source": f"profiles/traffic_{args.config}.json" if traffic else None,
                      "algorithmic_bytes_per_launch": nbytes["gateup"],
                      "avg_launch_us": round(stage_us["gateup"], 3)},
         "stages_us": {k: round(v, 3) for k, v in stage_us.items()},

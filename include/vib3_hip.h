@@ -176,11 +176,10 @@ typedef struct vib3_moe_int4_layer {
 size_t vib3_moe_int4_workspace_bytes(const vib3_moe_int4_layer *layer);
 int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer *layer, void *stream);
 
-/* Same launches with hipEvent_t events[0..3] (any may be NULL) recorded on `stream` before the
- * router, after the router, after the gate/up kernel and after the down kernel, so each stage
- * can be timed on the stream it runs on. */
-int vib3_launch_moe_int4_layer_timed(const vib3_moe_int4_layer *layer, void *stream,
-                                     void *const *events);
+/* One stage of the same layer: 0 = router (logits and, when separate, selection), 1 = fused
+ * gate/up + SwiGLU, 2 = down + weighted combine. A stage reads what the earlier stages of a
+ * previous call left in the workspace; for timing each stage's kernels on their own. */
+int vib3_launch_moe_int4_layer_stage(const vib3_moe_int4_layer *layer, int stage, void *stream);
 
 /* ------------------------------------------------------------------------------------------
  * Utilities

@@ -63,7 +63,7 @@ SIGNATURES = {
     "vib3_launch_router_topk_ex": (I, [P, I, P, I, P, I, I, I, I, F, I, P, P, P, P, P]),
     "vib3_moe_int4_workspace_bytes": (S, [C.POINTER(MoeInt4Layer)]),
     "vib3_launch_moe_int4_layer": (I, [C.POINTER(MoeInt4Layer), P]),
-    "vib3_launch_moe_int4_layer_timed": (I, [C.POINTER(MoeInt4Layer), P, C.POINTER(P)]),
+    "vib3_launch_moe_int4_layer_stage": (I, [C.POINTER(MoeInt4Layer), I, P]),
     "vib3_hip_zero": (I, [P, S, P]),
     "vib3_synth_bytes": (I, [P, S, U64, U64, S, P]),
     "vib3_synth_normal": (I, [P, I, S, U64, U64, S, F, P]),

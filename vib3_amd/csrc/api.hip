@@ -250,7 +250,9 @@ size_t vib3_moe_int4_workspace_bytes(const vib3_moe_int4_layer* L) {
   return layer_ws(L).total;
 }
 
-static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, void* const* events) {
+// only < 0: the whole layer; only = 0 / 1 / 2: just the router / gate-up / down launches, which
+// read what the earlier stages of a previous call left in the workspace (stage timing).
+static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) {
   if (!L) return VIB3_ERR_BAD_POINTER;
   if (!valid_act_dt(L->x_dtype) || !valid_scale_dt(L->scale_dtype)) return VIB3_ERR_UNSUPPORTED;
   if (L->hidden <= 0 || L->inter <= 0 || L->group_size <= 0 || L->top_k < 0 ||
@@ -274,10 +276,7 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, void* cons
   if (L->workspace_bytes < w.total) return VIB3_ERR_WORKSPACE;
   char* ws = (char*)L->workspace;
   hipStream_t st = S(stream);
-  auto mark = [&](int i) {
-    if (events && events[i]) (void)hipEventRecord((hipEvent_t)events[i], st);
-  };
-  mark(0);
+  auto run = [&](int i) { return only < 0 || only == i; };
 
   const uint16_t* ids = (const uint16_t*)(ws + w.ids);
   const float* wts = (const float*)(ws + w.wts);
@@ -300,14 +299,16 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, void* cons
       router.wts = (float*)(ws + w.wts);
       router.out_ids = L->out_ids;
       router.out_wts = L->out_weights;
-      int rc = launch_router_logits(router, st);
-      if (rc) return rc;
       // small expert counts select inside the gate/up kernel; larger ones need a launch
       route_in_kernel = L->num_experts <= kMaxExpertsInKernel && L->hidden <= 256 * 32;
       if (const char* v = getenv("VIB3_ROUTE_IN_KERNEL")) route_in_kernel &= atoi(v) != 0;
-      if (!route_in_kernel) {
-        rc = launch_router_select(router, st);
+      if (run(0)) {
+        int rc = launch_router_logits(router, st);
         if (rc) return rc;
+        if (!route_in_kernel) {
+          rc = launch_router_select(router, st);
+          if (rc) return rc;
+        }
       }
     } else {
       if (!L->in_ids || !L->in_weights) return VIB3_ERR_BAD_POINTER;
@@ -316,7 +317,6 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, void* cons
     }
   }
 
-  mark(1);
   const int h_dt = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? VIB3_DT_F32 : VIB3_DT_F16;
   RowsArgs a{};
   a.x = L->x; a.x_dt = L->x_dtype; a.K = L->hidden; a.M = L->inter; a.g = L->group_size;
@@ -330,9 +330,10 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, void* cons
   a.out = ws + w.h; a.out_dt = h_dt; a.out_stride = (size_t)L->inter;
   a.route = route_in_kernel;
   a.router = router;
-  int rc = launch_rows(a, true, st);
-  if (rc) return rc;
-  mark(2);
+  if (run(1)) {
+    int rc = launch_rows(a, true, st);
+    if (rc) return rc;
+  }
 
   DownArgs d{};
   d.h = ws + w.h; d.h_dt = h_dt; d.K = L->inter; d.M = L->hidden; d.g = L->group_size;
@@ -342,18 +343,16 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, void* cons
   d.magic = page_magic(L->rows_per_page[2]);
   d.round_f16 = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? 0 : 1;
   d.out = L->out;
-  rc = launch_down(d, st);
-  mark(3);
-  return rc;
+  return run(2) ? launch_down(d, st) : 0;
 }
 
 int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
-  return moe_int4_layer(L, stream, nullptr);
+  return moe_int4_layer(L, stream, -1);
 }
 
-int vib3_launch_moe_int4_layer_timed(const vib3_moe_int4_layer* L, void* stream,
-                                     void* const* events) {
-  return moe_int4_layer(L, stream, events);
+int vib3_launch_moe_int4_layer_stage(const vib3_moe_int4_layer* L, int stage, void* stream) {
+  if (stage < 0 || stage > 2) return VIB3_ERR_BAD_COUNT;
+  return moe_int4_layer(L, stream, stage);
 }
 
 }  // extern "C"

@@ -757,7 +757,7 @@ static int env_int(const char* name, int dflt) {
 }
 
 template <int N, bool D, bool S, bool P>
-static void launch_rows_p(RowsArgs& a, hipStream_t s) {
+static void launch_rows_p(RowsArgs& a, hipStream_t s, KTime t) {
   if (a.KS == 1) {
     auto k = k_int4_rows<N, D, S, P>;
     const int items = a.nslots * a.M;
@@ -767,22 +767,23 @@ static void launch_rows_p(RowsArgs& a, hipStream_t s) {
     if (per_cu > 0 && per_cu * device_cus() < cap) cap = per_cu * device_cus();
     const int floor_blocks = (items + 4 * kWave - 1) / (4 * kWave);  // <= 64 items per wave
     if (cap < floor_blocks) cap = floor_blocks;
-    hipLaunchKernelGGL(k, dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0, s, a);
+    hipExtLaunchKernelGGL(k, dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0, s, t.start,
+                          t.stop, 0, a);
   } else {
     auto k = k_int4_rows_ksplit<N, D, S, P>;
     const int teams = 4 / a.KS;
     dim3 grid((unsigned)((a.M + teams * a.RPT - 1) / (teams * a.RPT)), (unsigned)a.nslots);
-    hipLaunchKernelGGL(k, grid, dim3(256), 0, s, a);
+    hipExtLaunchKernelGGL(k, grid, dim3(256), 0, s, t.start, t.stop, 0, a);
   }
 }
 
 
 template <int N, bool D, bool S>
-static void launch_rows_t(RowsArgs& a, hipStream_t s) {
-  if (!a.routed_table) return launch_rows_p<N, D, S, false>(a, s);
-  return launch_rows_p<N, D, S, true>(a, s);
+static void launch_rows_t(RowsArgs& a, hipStream_t s, KTime t) {
+  if (!a.routed_table) return launch_rows_p<N, D, S, false>(a, s, t);
+  return launch_rows_p<N, D, S, true>(a, s, t);
 }
-int launch_rows(RowsArgs a, bool dual, hipStream_t s) {
+int launch_rows(RowsArgs a, bool dual, hipStream_t s, KTime t) {
   const int cpr = a.K / 32;
   int nch = 1, ks = 1;
   if (pick_nch(cpr, 4, nch, ks)) return VIB3_ERR_UNSUPPORTED;
@@ -792,8 +793,8 @@ int launch_rows(RowsArgs a, bool dual, hipStream_t s) {
   const bool split = a.x_dt == VIB3_DT_F32;
 #define VIB3_ROWS(N, D)                                   \
   do {                                                    \
-    if (split) launch_rows_t<N, D, true>(a, s);           \
-    else launch_rows_t<N, D, false>(a, s);                \
+    if (split) launch_rows_t<N, D, true>(a, s, t);        \
+    else launch_rows_t<N, D, false>(a, s, t);             \
   } while (0)
   if (dual) {
     if (nch == 1) VIB3_ROWS(1, true);
@@ -809,7 +810,7 @@ int launch_rows(RowsArgs a, bool dual, hipStream_t s) {
 }
 
 template <bool S, bool W>
-static void launch_down_t(DownArgs& a, hipStream_t s) {
+static void launch_down_t(DownArgs& a, hipStream_t s, KTime t) {
   auto k = k_down_combine<S, W>;
   const int block = a.nslots * a.KS * kWave;
   int cap = resident_blocks(k, block);
@@ -822,8 +823,8 @@ static void launch_down_t(DownArgs& a, hipStream_t s) {
   if (rb > kWave) rb = kWave;
   a.RB = rb;
   const int blocks = (a.M + rb - 1) / rb;
-  hipLaunchKernelGGL(k, dim3((unsigned)(blocks < cap ? blocks : cap)), dim3((unsigned)block), 0,
-                     s, a);
+  hipExtLaunchKernelGGL(k, dim3((unsigned)(blocks < cap ? blocks : cap)), dim3((unsigned)block), 0,
+                        s, t.start, t.stop, 0, a);
 }
 
 #ifndef VIB3_DOWN_ROWS_BUFFERS
@@ -835,23 +836,23 @@ constexpr int kDownRowsBuffers = VIB3_DOWN_ROWS_BUFFERS;
 static size_t down_rows_lds(int nslots, int J) { return (size_t)nslots * 16 * J * (64 + 4); }
 
 template <int J>
-static void launch_down_rows_t(DownArgs& a, hipStream_t s) {
+static void launch_down_rows_t(DownArgs& a, hipStream_t s, KTime t) {
   const int groups = (a.M + 3) / 4;
   const int blocks = (groups + 3) / 4;
-  hipLaunchKernelGGL((k_down_rows<J, kDownRowsBuffers>), dim3((unsigned)blocks), dim3(256),
-                     (unsigned)down_rows_lds(a.nslots, J), s, a);
+  hipExtLaunchKernelGGL((k_down_rows<J, kDownRowsBuffers>), dim3((unsigned)blocks), dim3(256),
+                        (unsigned)down_rows_lds(a.nslots, J), s, t.start, t.stop, 0, a);
 }
 
-int launch_down(DownArgs a, hipStream_t s) {
+int launch_down(DownArgs a, hipStream_t s, KTime t) {
   const int cpr = a.K / 32;
   if (a.M <= 0) return 0;
   // staged-activation kernel for f16 intermediates of up to 64 chunks per row
   const int J = cpr <= 16 ? 1 : cpr <= 32 ? 2 : cpr <= 64 ? 4 : 0;
   if (a.h_dt == VIB3_DT_F16 && J && down_rows_lds(a.nslots, J) <= 64 * 1024 &&
       env_int("VIB3_DOWN_COMBINE", 0) == 0) {
-    if (J == 1) launch_down_rows_t<1>(a, s);
-    else if (J == 2) launch_down_rows_t<2>(a, s);
-    else launch_down_rows_t<4>(a, s);
+    if (J == 1) launch_down_rows_t<1>(a, s, t);
+    else if (J == 2) launch_down_rows_t<2>(a, s, t);
+    else launch_down_rows_t<4>(a, s, t);
     VIB3_RETURN_LAUNCH();
   }
   const int ks = (cpr + kDownSpan - 1) / kDownSpan;
@@ -860,11 +861,11 @@ int launch_down(DownArgs a, hipStream_t s) {
   if (a.M <= 0) return 0;
   const bool wide = a.nslots * ks > 10;
   if (a.h_dt == VIB3_DT_F32) {
-    if (wide) launch_down_t<true, true>(a, s);
-    else launch_down_t<true, false>(a, s);
+    if (wide) launch_down_t<true, true>(a, s, t);
+    else launch_down_t<true, false>(a, s, t);
   } else {
-    if (wide) launch_down_t<false, true>(a, s);
-    else launch_down_t<false, false>(a, s);
+    if (wide) launch_down_t<false, true>(a, s, t);
+    else launch_down_t<false, false>(a, s, t);
   }
   VIB3_RETURN_LAUNCH();
 }

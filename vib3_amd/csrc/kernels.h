@@ -1,12 +1,19 @@
 // kernels.h — argument blocks and internal launchers shared by the .hip translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "common.h"
 
 namespace vib3 {
+
+// Optional timing of one launch: events recorded by the dispatch itself at kernel begin / end
+// (hipExtLaunchKernel), so the interval is the kernel's own duration on its stream.
+struct KTime {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
 
 // Router: logits (one workgroup per expert) and top-k selection (one wavefront, select.h).
 struct RouterArgs {
@@ -25,8 +32,8 @@ struct RouterArgs {
   float* out_wts;
 };
 
-int launch_router_logits(const RouterArgs& a, hipStream_t s);
-int launch_router_select(const RouterArgs& a, hipStream_t s);
+int launch_router_logits(const RouterArgs& a, hipStream_t s, KTime t = {});
+int launch_router_select(const RouterArgs& a, hipStream_t s, KTime t = {});
 
 // Experts whose selection fits the register path of select.h (8 keys per lane).
 constexpr int kMaxExpertsInKernel = 8 * 64;
@@ -89,8 +96,8 @@ struct GenericArgs {
   int out_dt;
 };
 
-int launch_rows(RowsArgs a, bool dual, hipStream_t s);
-int launch_down(DownArgs a, hipStream_t s);
+int launch_rows(RowsArgs a, bool dual, hipStream_t s, KTime t = {});
+int launch_down(DownArgs a, hipStream_t s, KTime t = {});
 int launch_generic(GenericArgs a, bool dual, hipStream_t s);
 
 constexpr int kMaxExperts = 4096;

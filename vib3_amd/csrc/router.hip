@@ -108,14 +108,16 @@ __global__ __launch_bounds__(64) void k_router_select(RouterArgs a) {
   else select_topk_lds(a, a.scores, sel, wts, true);
 }
 
-int launch_router_logits(const RouterArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_router_logits, dim3((unsigned)a.E), dim3(256), 0, s, a);
+int launch_router_logits(const RouterArgs& a, hipStream_t s, KTime t) {
+  hipExtLaunchKernelGGL(k_router_logits, dim3((unsigned)a.E), dim3(256), 0, s, t.start, t.stop, 0, a);
   VIB3_RETURN_LAUNCH();
 }
 
-int launch_router_select(const RouterArgs& a, hipStream_t s) {
-  if (a.E <= 8 * kWave) hipLaunchKernelGGL(k_router_select<true>, dim3(1), dim3(64), 0, s, a);
-  else hipLaunchKernelGGL(k_router_select<false>, dim3(1), dim3(64), 0, s, a);
+int launch_router_select(const RouterArgs& a, hipStream_t s, KTime t) {
+  if (a.E <= 8 * kWave)
+    hipExtLaunchKernelGGL(k_router_select<true>, dim3(1), dim3(64), 0, s, t.start, t.stop, 0, a);
+  else
+    hipExtLaunchKernelGGL(k_router_select<false>, dim3(1), dim3(64), 0, s, t.start, t.stop, 0, a);
   VIB3_RETURN_LAUNCH();
 }
 
