@@ -182,6 +182,33 @@ int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer *layer, void *stream);
 int vib3_launch_moe_int4_layer_stage(const vib3_moe_int4_layer *layer, int stage, void *stream);
 
 /* ------------------------------------------------------------------------------------------
+ * Batched decode over MXFP4 experts (no counterpart in cuda_ffi.rs): T tokens, top_k picks
+ * each, grouped per expert and run as a grouped GEMM on the CDNA4 matrix cores.
+ * Per token t: h = f16(silu(gate_e . x_t) * (up_e . x_t)), d_j = f16(down_e . h),
+ * out[t] = bf16(sum_j w[t,j] * d_j) in pick order: the per-token composition of engine.rs
+ * (execute_expert, :5801-6306) with MXFP4 weights, E2M1 codes (kernels.cu:438-441, low nibble =
+ * even k) times E8M0 scales 2^(e-127) per 32 along k (kernels.cu:2770-2777).
+ * MXFP4 page: [rows x k/2] code bytes, then [rows x k/32] E8M0 bytes.
+ * ---------------------------------------------------------------------------------------- */
+typedef struct vib3_moe_mxfp4_batch {
+    const void *x;           /* [tokens][hidden] bf16, 16-byte aligned */
+    int tokens;
+    int hidden;              /* multiple of 256 */
+    int inter;               /* multiple of 128 */
+    int num_experts;         /* <= 4096 */
+    int top_k;               /* tokens * top_k <= 4096 */
+    const uint16_t *ids;     /* [tokens][top_k] device; ids >= num_experts are skipped */
+    const float *weights;    /* [tokens][top_k] device */
+    const uint64_t *page_table; /* [num_experts][3] device: up, gate, down MXFP4 pages */
+    void *out;               /* [tokens][hidden] bf16 */
+    void *workspace;         /* vib3_moe_mxfp4_workspace_bytes() bytes, 256-byte aligned */
+    size_t workspace_bytes;
+} vib3_moe_mxfp4_batch;
+
+size_t vib3_moe_mxfp4_workspace_bytes(const vib3_moe_mxfp4_batch *batch);
+int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch *batch, void *stream);
+
+/* ------------------------------------------------------------------------------------------
  * Utilities
  * ---------------------------------------------------------------------------------------- */
 
@@ -200,6 +227,11 @@ int vib3_synth_normal(void *dst, int dtype, size_t n, uint64_t seed, uint64_t st
 int vib3_synth_int4_page(void *page, uint64_t seed, uint64_t stream, int k, int group_size,
                          int scale_dtype, float sigma, int row_start, int rows,
                          void *hip_stream);
+
+/* Rows [row_start, row_start + rows) of the logical MXFP4 matrix `stream` (k columns) as one
+ * page: code bytes from stream*2, E8M0 bytes 119 + hash % 5 (2^-8 .. 2^-4) from stream*2+1. */
+int vib3_synth_mxfp4_page(void *page, uint64_t seed, uint64_t stream, int k, int row_start,
+                          int rows, void *hip_stream);
 
 /* Library version string. */
 const char *vib3_hip_version(void);

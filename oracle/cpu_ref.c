@@ -480,6 +480,44 @@ void v3o_matmul_mxfp4_acc(const float *x, const uint8_t *codes, const uint8_t *s
     parallel_rows(m, nthreads, mx_rows, &c);
 }
 
+/* Batched MoE over MXFP4 experts, restated per token the way the engine decodes (there is no
+ * multi-token MoE in the reference): per token, each pick runs execute_expert's composition
+ * (engine.rs:5801-6306) with MXFP4 matrices, f16 rounding of h and d (kernels.rs:3042, :2825),
+ * then weighted_accumulate_f32 in pick order (kernels.rs:2033); out is rounded to bf16. */
+void v3o_moe_mxfp4_batched(const float *x, size_t tokens, size_t hidden, size_t inter,
+                           const uint8_t *const *pages, size_t num_experts, const uint16_t *ids,
+                           const float *weights, size_t top_k, uint16_t *out, int nthreads)
+{
+    float *gate = (float *)malloc(sizeof(float) * inter);
+    float *up = (float *)malloc(sizeof(float) * inter);
+    float *h = (float *)malloc(sizeof(float) * inter);
+    float *d = (float *)malloc(sizeof(float) * hidden);
+    float *o = (float *)malloc(sizeof(float) * hidden);
+    for (size_t t = 0; t < tokens; t++) {
+        const float *xt = x + t * hidden;
+        memset(o, 0, sizeof(float) * hidden);
+        for (size_t j = 0; j < top_k; j++) {
+            size_t e = ids[t * top_k + j];
+            if (e >= num_experts) continue;
+            const uint8_t *pu = pages[e * 3 + 0], *pg = pages[e * 3 + 1], *pd = pages[e * 3 + 2];
+            v3o_matmul_mxfp4_acc(xt, pu, pu + inter * (hidden / 2), hidden, inter, up, nthreads);
+            v3o_matmul_mxfp4_acc(xt, pg, pg + inter * (hidden / 2), hidden, inter, gate, nthreads);
+            for (size_t r = 0; r < inter; r++)
+                h[r] = v3o_f16_to_f32(v3o_f32_to_f16(silu_times(gate[r], up[r])));
+            v3o_matmul_mxfp4_acc(h, pd, pd + hidden * (inter / 2), inter, hidden, d, nthreads);
+            float w = weights[t * top_k + j];
+            for (size_t r = 0; r < hidden; r++)
+                o[r] += w * v3o_f16_to_f32(v3o_f32_to_f16(d[r]));
+        }
+        for (size_t r = 0; r < hidden; r++) out[t * hidden + r] = v3o_f32_to_bf16(o[r]);
+    }
+    free(gate);
+    free(up);
+    free(h);
+    free(d);
+    free(o);
+}
+
 /* ------------------------------------------------------------------ synthetic data */
 
 static inline uint64_t mix64(uint64_t z)
@@ -551,4 +589,20 @@ void v3o_synth_int4_page(uint64_t seed, uint64_t stream, size_t k, size_t g, int
         sc[2 * i] = (uint8_t)(b & 0xff);
         sc[2 * i + 1] = (uint8_t)(b >> 8);
     }
+}
+
+/* E8M0 bytes 119 + hash % 5 (2^-8 .. 2^-4), as csrc/synth.hip's k_synth_e8m0. */
+uint8_t v3o_synth_e8m0(uint64_t seed, uint64_t stream, uint64_t idx)
+{
+    return (uint8_t)(119 + v3o_synth_hash(seed, stream, idx) % 5);
+}
+
+void v3o_synth_mxfp4_page(uint64_t seed, uint64_t stream, size_t k, size_t row_start, size_t rows,
+                          uint8_t *page)
+{
+    size_t pk = k / 2, nb = k / 32;
+    v3o_synth_bytes(seed, stream * 2, row_start * pk, rows * pk, page);
+    uint8_t *sc = page + rows * pk;
+    for (size_t i = 0; i < rows * nb; i++)
+        sc[i] = v3o_synth_e8m0(seed, stream * 2 + 1, row_start * nb + i);
 }

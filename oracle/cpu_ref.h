@@ -119,6 +119,13 @@ float v3o_e8m0(uint8_t e);
 void v3o_matmul_mxfp4_acc(const float *x, const uint8_t *codes, const uint8_t *scales, size_t k,
                           size_t m, float *acc, int nthreads);
 
+/* Batched MoE over MXFP4 experts (c4), restated per token: pages[e*3 + {0 up, 1 gate, 2 down}]
+ * are MXFP4 pages ([rows x k/2] codes, then [rows x k/32] E8M0 bytes); x is [tokens][hidden];
+ * picks with ids >= num_experts are skipped; out is [tokens][hidden] bf16. */
+void v3o_moe_mxfp4_batched(const float *x, size_t tokens, size_t hidden, size_t inter,
+                           const uint8_t *const *pages, size_t num_experts, const uint16_t *ids,
+                           const float *weights, size_t top_k, uint16_t *out, int nthreads);
+
 /* ---- synthetic data generator (counter-based, identical spec in csrc/synth.hip) ---- */
 uint64_t v3o_synth_hash(uint64_t seed, uint64_t stream, uint64_t ctr);
 float v3o_synth_normal(uint64_t seed, uint64_t stream, uint64_t ctr);
@@ -132,6 +139,12 @@ void v3o_synth_normal_array(uint64_t seed, uint64_t stream, size_t off, size_t n
 /* Write rows [row_start, row_start+rows) of the logical INT4 matrix (stream, k, g) as one page. */
 void v3o_synth_int4_page(uint64_t seed, uint64_t stream, size_t k, size_t g, int scale_dt,
                          float sigma, size_t row_start, size_t rows, uint8_t *page);
+
+/* E8M0 scale byte 119 + hash % 5 (2^-8 .. 2^-4) and an MXFP4 page of the logical matrix
+ * `stream`: codes from stream*2 (uniform over all 16), scales from stream*2+1. */
+uint8_t v3o_synth_e8m0(uint64_t seed, uint64_t stream, uint64_t idx);
+void v3o_synth_mxfp4_page(uint64_t seed, uint64_t stream, size_t k, size_t row_start, size_t rows,
+                          uint8_t *page);
 
 #ifdef __cplusplus
 }

@@ -60,6 +60,9 @@ def _declare(L: C.CDLL) -> None:
         "v3o_synth_scale": (C.c_uint16, [U64, U64, U64, F, I]),
         "v3o_synth_normal_array": (None, [U64, U64, S, S, F, I, P]),
         "v3o_synth_int4_page": (None, [U64, U64, S, S, I, F, S, S, P]),
+        "v3o_moe_mxfp4_batched": (None, [P, S, S, S, P, S, P, P, S, P, I]),
+        "v3o_synth_e8m0": (C.c_uint8, [U64, U64, U64]),
+        "v3o_synth_mxfp4_page": (None, [U64, U64, S, S, S, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -256,4 +259,29 @@ def synth_int4_page(seed, stream, k, g, scale_dt, sigma, row_start, rows) -> np.
     pk, ng = (k + 1) // 2, (k + g - 1) // g
     out = np.empty(rows * pk + rows * ng * 2, dtype=np.uint8)
     lib().v3o_synth_int4_page(seed, stream, k, g, scale_dt, float(sigma), row_start, rows, _p(out))
+    return out
+
+
+def synth_mxfp4_page(seed, stream, k, row_start, rows) -> np.ndarray:
+    """MXFP4 page ([rows x k/2] codes, then [rows x k/32] E8M0 bytes) of logical matrix `stream`."""
+    out = np.empty(rows * (k // 2) + rows * (k // 32), dtype=np.uint8)
+    lib().v3o_synth_mxfp4_page(seed, stream, k, row_start, rows, _p(out))
+    return out
+
+
+def moe_mxfp4_batched(x, hidden, inter, pages, ids, weights, nthreads=0) -> np.ndarray:
+    """Per-token restatement of the batched MXFP4 MoE (see cpu_ref.h); returns bf16 bits.
+
+    x: [tokens, hidden] f32 (the bf16 activations, widened); pages: list over experts of
+    (up, gate, down) uint8 pages; ids / weights: [tokens, top_k]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    tokens = x.shape[0]
+    ids = np.ascontiguousarray(ids, dtype=np.uint16)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    top_k = ids.shape[1]
+    keep = [np.ascontiguousarray(p, dtype=np.uint8) for trio in pages for p in trio]
+    arr = (C.c_void_p * len(keep))(*[k.ctypes.data for k in keep])
+    out = np.empty((tokens, hidden), dtype=np.uint16)
+    lib().v3o_moe_mxfp4_batched(_p(x), tokens, hidden, inter, C.cast(arr, C.c_void_p),
+                                len(pages), _p(ids), _p(weights), top_k, _p(out), nthreads)
     return out

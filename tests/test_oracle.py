@@ -316,6 +316,56 @@ def test_matmul_mxfp4_bruteforce():
     assert np.allclose(got, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
 
 
+def _mx_dense(page, rows, k):
+    """f64 dense matrix of an MXFP4 page (independent of the oracle's C decode)."""
+    lut = np.array([(-1.0 if c & 8 else 1.0) * [0, 0.5, 1, 1.5, 2, 3, 4, 6][c & 7]
+                    for c in range(16)])
+    codes = page[: rows * k // 2].reshape(rows, k // 2)
+    sc = page[rows * k // 2: rows * k // 2 + rows * k // 32].reshape(rows, k // 32)
+    q = np.empty((rows, k), dtype=np.int64)
+    q[:, 0::2] = codes & 15
+    q[:, 1::2] = codes >> 4
+    return lut[q] * np.repeat(2.0 ** (sc.astype(np.float64) - 127), 32, axis=1)
+
+
+def test_moe_mxfp4_batched_matches_dense_f64():
+    """The per-token MXFP4 composition against an f64 recomputation with the same f16 rounding
+    points (h and each expert output); a skipped out-of-range pick contributes nothing."""
+    hidden, inter, E, T, k = 128, 96, 6, 3, 3
+    pages = [tuple(O.synth_mxfp4_page(5, 3 * e + s, *( (hidden, 0, inter) if s < 2 else (inter, 0, hidden)))
+                   for s in range(3)) for e in range(E)]
+    rng = np.random.default_rng(4)
+    x = O.to_f32(O.synth_normal_array(5, 99, 0, T * hidden, 1.0, O.BF16), O.BF16).reshape(T, hidden)
+    ids = np.array([[0, 3, 5], [2, 2, 1], [4, E, 0]], dtype=np.uint16)  # E = out of range
+    w = rng.random((T, k)).astype(np.float32)
+    got = O.to_f32(O.moe_mxfp4_batched(x, hidden, inter, pages, ids, w).ravel(), O.BF16).reshape(T, hidden)
+    ref = np.zeros((T, hidden))
+    for t in range(T):
+        for j in range(k):
+            e = int(ids[t, j])
+            if e >= E:
+                continue
+            up = _mx_dense(pages[e][0], inter, hidden) @ x[t]
+            gate = _mx_dense(pages[e][1], inter, hidden) @ x[t]
+            h = (gate / (1 + np.exp(-gate)) * up).astype(np.float16).astype(np.float64)
+            d = (_mx_dense(pages[e][2], hidden, inter) @ h).astype(np.float16).astype(np.float64)
+            ref[t] += w[t, j] * d
+    # bf16 output rounding (2^-9) dominates; a wrong term, sign or index is far outside it
+    assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-4 * np.abs(ref).max())
+
+
+def test_synth_mxfp4_page():
+    k, rows = 256, 24
+    page = O.synth_mxfp4_page(7, 5, k, 0, rows)
+    assert np.array_equal(page[: rows * k // 2], O.synth_bytes(7, 10, 0, rows * k // 2))
+    sc = page[rows * k // 2:]
+    assert sc.size == rows * k // 32 and sc.min() >= 119 and sc.max() <= 123
+    assert np.all(np.bincount(sc, minlength=124)[119:] > 0)
+    part = O.synth_mxfp4_page(7, 5, k, 8, 4)  # rows 8..11 cut from the same logical matrix
+    assert np.array_equal(part[: 4 * k // 2], page[8 * k // 2: 12 * k // 2])
+    assert np.array_equal(part[4 * k // 2:], sc[8 * k // 32: 12 * k // 32])
+
+
 # ---------------------------------------------------------------- synthetic generator
 
 def test_synth_normal_moments_and_scales():

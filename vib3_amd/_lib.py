@@ -46,6 +46,17 @@ class MoeInt4Layer(C.Structure):
     ]
 
 
+class MoeMxfp4Batch(C.Structure):
+    """vib3_moe_mxfp4_batch (include/vib3_hip.h)."""
+
+    _fields_ = [
+        ("x", C.c_void_p), ("tokens", C.c_int), ("hidden", C.c_int), ("inter", C.c_int),
+        ("num_experts", C.c_int), ("top_k", C.c_int), ("ids", C.c_void_p),
+        ("weights", C.c_void_p), ("page_table", C.c_void_p), ("out", C.c_void_p),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
 # name -> (restype, argtypes); every symbol declared in include/vib3_hip.h
 P, I, F, S, U64 = C.c_void_p, C.c_int, C.c_float, C.c_size_t, C.c_uint64
 SIGNATURES = {
@@ -64,10 +75,13 @@ SIGNATURES = {
     "vib3_moe_int4_workspace_bytes": (S, [C.POINTER(MoeInt4Layer)]),
     "vib3_launch_moe_int4_layer": (I, [C.POINTER(MoeInt4Layer), P]),
     "vib3_launch_moe_int4_layer_stage": (I, [C.POINTER(MoeInt4Layer), I, P]),
+    "vib3_moe_mxfp4_workspace_bytes": (S, [C.POINTER(MoeMxfp4Batch)]),
+    "vib3_launch_moe_mxfp4_batched": (I, [C.POINTER(MoeMxfp4Batch), P]),
     "vib3_hip_zero": (I, [P, S, P]),
     "vib3_synth_bytes": (I, [P, S, U64, U64, S, P]),
     "vib3_synth_normal": (I, [P, I, S, U64, U64, S, F, P]),
     "vib3_synth_int4_page": (I, [P, U64, U64, I, I, I, F, I, I, P]),
+    "vib3_synth_mxfp4_page": (I, [P, U64, U64, I, I, I, P]),
     "vib3_hip_version": (C.c_char_p, []),
 }
 

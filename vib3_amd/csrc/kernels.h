@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "common.h"
+#include "../../include/vib3_hip.h"
 
 namespace vib3 {
 

@@ -1,0 +1,385 @@
+// mxfp4_moe.hip — batched MoE decode over MXFP4 experts as a grouped GEMM on MFMA.
+//
+// T tokens each pick top_k experts (ids and weights given on the device). Tokens are grouped
+// per expert, then every touched expert streams its weights once for all of its tokens:
+//   h[t]   = f16( silu(gate_e . x_t) * (up_e . x_t) )     fused gate/up + SwiGLU
+//   d[t,j] = f16( down_e . h[t] )
+//   out[t] = bf16( sum_j w[t,j] * d[t,j] )                 in pick order, o = o + w*d
+// which is the reference's per-token composition (engine.rs:5801-6306 execute_expert, the
+// f16 rounding points of kernels.rs:3042 / :2825, weighted_accumulate_f32 kernels.rs:2000)
+// applied to MXFP4 weights: E2M1 codes (kernels.cu:438-441, low nibble = even k) times an
+// E8M0 scale 2^(e-127) per 32 along k (kernels.cu:2770-2777).
+//
+// MXFP4 page: [rows x K/2] code bytes, then [rows x K/32] E8M0 bytes.
+//
+// The contraction runs on the CDNA4 matrix cores: weights are decoded in registers with
+// v_cvt_scalef32_pk_{bf16,f16}_fp4 (exact: every E2M1 x 2^e value of the scale range is a
+// bf16 / f16 number) and fed to v_mfma_f32_16x16x32_{bf16,f16} against the tokens' bf16
+// activations (gate/up) or f16 intermediates (down). Products are exact and accumulate in f32,
+// so results differ from the sequential CPU sum only by the order of f32 additions.
+#include <hip/hip_ext.h>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace vib3 {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMxTokBlk = 16;            // tokens per MFMA column block
+constexpr int kMxMaxBlk = 4;             // column blocks per pass (64 tokens)
+constexpr int kMxStep = 128;             // k per step: 4 lane groups x 32
+constexpr int kMxTiles = 4;              // 16-row A tiles per wave
+constexpr int kMxMaxPicks = 4096;        // tokens * top_k per launch (grouping is one workgroup)
+
+struct MxArgs {
+  const uint16_t* x;          // [T][hidden] bf16
+  const uint64_t* table;      // [E][3] page addresses: up, gate, down
+  const int* d_expert;        // [nd] expert of distinct index d
+  const int* d_off;           // [nd] first entry of d
+  const int* d_cnt;           // [nd] entries of d
+  const int* nd;              // number of distinct experts
+  const int* ent_tok;         // [T*top_k] token of each entry (grouped by expert)
+  const int* ent_slot;        // [T*top_k] t*top_k + j of each entry
+  const uint16_t* zero;       // zero row (>= max(hidden, inter) halves)
+  uint16_t* h;                // [T*top_k][inter] f16, by entry
+  uint16_t* d;                // [T*top_k][hidden] f16, by slot
+  int hidden, inter;
+};
+
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  const u32x4 v = *(const __attribute__((address_space(1))) u32x4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint8_t ld_u8(const uint8_t* p) {
+  return *(const __attribute__((address_space(1))) uint8_t*)p;
+}
+
+__device__ __forceinline__ float e8m0_scale(uint8_t e) {
+  return __uint_as_float((uint32_t)e << 23);
+}
+
+// Eight E2M1 codes (one 32-bit word, low nibble first) times `scale` as bf16 / f16 operands.
+template <bool BF16>
+__device__ __forceinline__ void decode8(uint32_t w, float scale, bf16x8_t& ob, f16x8_t& oh) {
+  if (BF16) {
+    const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
+    const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
+    const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
+    const bf16x2_t e = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
+    ob = bf16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], e[0], e[1]};
+  } else {
+    const f16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 0);
+    const f16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 1);
+    const f16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 2);
+    const f16x2_t e = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 3);
+    oh = f16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], e[0], e[1]};
+  }
+}
+
+// One wave: kMxTiles tiles of 16 weight rows x all the expert's tokens (in passes of 64).
+// GATEUP: tiles 0,1 = up rows r0..r0+31, tiles 2,3 = gate rows r0..r0+31 (bf16 MFMA on x);
+// otherwise tiles 0..3 = down rows r0..r0+63 (f16 MFMA on h).
+//
+// Operand layout of v_mfma_f32_16x16x32: lane l supplies A row (l & 15), k block (l >> 4)
+// of 8 values, and B column (l & 15), the same k block. Each lane loads the 16 bytes = 32
+// codes of its row at k = step*128 + (l >> 4)*32, and MFMA s (0..3) takes the s-th word: the
+// four k blocks of one MFMA are then k = step*128 + g*32 + s*8 (g = lane group), a fixed
+// permutation of the step's k range that A and B share. The scale of the whole 32-code chunk
+// is one E8M0 byte. Result D: lane l holds rows (l >> 4)*4 + i, column l & 15.
+template <bool GATEUP>
+__global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
+  const int dix = (int)blockIdx.x;
+  if (dix >= *a.nd) return;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int rr = lane & 15, g = lane >> 4;
+  const int e = a.d_expert[dix], o_e = a.d_off[dix], t_e = a.d_cnt[dix];
+  const int K = GATEUP ? a.hidden : a.inter;   // reduction
+  const int M = GATEUP ? a.inter : a.hidden;   // rows of each matrix
+  const int rows_per_wave = GATEUP ? 32 : 64;
+  const int r0 = ((int)blockIdx.y * 4 + wave) * rows_per_wave;
+  if (r0 >= M) return;
+  const size_t pkb = (size_t)K / 2, nsb = (size_t)K / 32;
+  const uint8_t* m0 = (const uint8_t*)a.table[(size_t)e * 3 + (GATEUP ? 0 : 2)];
+  const uint8_t* m1 = GATEUP ? (const uint8_t*)a.table[(size_t)e * 3 + 1] : m0;
+
+  // tile t: matrix base and row
+  const uint8_t* tcode[kMxTiles];
+  const uint8_t* tscale[kMxTiles];
+#pragma unroll
+  for (int t = 0; t < kMxTiles; t++) {
+    const uint8_t* base = GATEUP ? (t < 2 ? m0 : m1) : m0;
+    const int row = GATEUP ? r0 + (t & 1) * 16 + rr : r0 + t * 16 + rr;
+    tcode[t] = base + (size_t)row * pkb + (size_t)g * 16;
+    tscale[t] = base + (size_t)M * pkb + (size_t)row * nsb + g;
+  }
+
+  for (int p0 = 0; p0 < t_e; p0 += kMxTokBlk * kMxMaxBlk) {
+    const int nblk = min(kMxMaxBlk, (t_e - p0 + kMxTokBlk - 1) / kMxTokBlk);
+    // B rows of this lane's column in each block (zero row past the expert's tokens)
+    const uint16_t* brow[kMxMaxBlk];
+#pragma unroll
+    for (int b = 0; b < kMxMaxBlk; b++) {
+      const int tok = p0 + b * kMxTokBlk + rr;
+      const uint16_t* r = a.zero;
+      if (b < nblk && tok < t_e) {
+        r = GATEUP ? a.x + (size_t)a.ent_tok[o_e + tok] * K : a.h + (size_t)(o_e + tok) * K;
+      }
+      brow[b] = r + g * 32;
+    }
+    f32x4_t acc[kMxTiles][kMxMaxBlk];
+#pragma unroll
+    for (int t = 0; t < kMxTiles; t++)
+#pragma unroll
+      for (int b = 0; b < kMxMaxBlk; b++) acc[t][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int ks = 0; ks < K; ks += kMxStep) {
+      uint4 w[kMxTiles];
+      uint8_t sc[kMxTiles];
+#pragma unroll
+      for (int t = 0; t < kMxTiles; t++) {
+        w[t] = ld16(tcode[t] + ks / 2);
+        sc[t] = ld_u8(tscale[t] + ks / 32);
+      }
+      uint4 xb[kMxMaxBlk][4];
+#pragma unroll
+      for (int b = 0; b < kMxMaxBlk; b++) {
+        if (b < nblk) {
+#pragma unroll
+          for (int s = 0; s < 4; s++) xb[b][s] = ld16(brow[b] + ks + s * 8);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kMxTiles; t++) {
+        const float scale = e8m0_scale(sc[t]);
+        const uint32_t words[4] = {w[t].x, w[t].y, w[t].z, w[t].w};
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+          bf16x8_t ab;
+          f16x8_t ah;
+          decode8<GATEUP>(words[s], scale, ab, ah);
+#pragma unroll
+          for (int b = 0; b < kMxMaxBlk; b++) {
+            if (b < nblk) {
+              if (GATEUP) {
+                acc[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    ab, __builtin_bit_cast(bf16x8_t, xb[b][s]), acc[t][b], 0, 0, 0);
+              } else {
+                acc[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    ah, __builtin_bit_cast(f16x8_t, xb[b][s]), acc[t][b], 0, 0, 0);
+              }
+            }
+          }
+        }
+      }
+    }
+
+    // epilogue: lane holds rows (g*4 + i) of each tile for token column rr of each block
+#pragma unroll
+    for (int b = 0; b < kMxMaxBlk; b++) {
+      const int tok = p0 + b * kMxTokBlk + rr;
+      if (b >= nblk || tok >= t_e) continue;
+      if (GATEUP) {
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+          uint16_t hv[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float up = acc[half][b][i], gate = acc[2 + half][b][i];
+            hv[i] = f32_to_f16_bits((gate / (1.0f + expf(-gate))) * up);  // kernels.rs:3041
+          }
+          const int row = r0 + half * 16 + g * 4;
+          uint2 v = make_uint2((uint32_t)hv[0] | ((uint32_t)hv[1] << 16),
+                               (uint32_t)hv[2] | ((uint32_t)hv[3] << 16));
+          *(uint2*)(a.h + (size_t)(o_e + tok) * M + row) = v;
+        }
+      } else {
+        const int slot = a.ent_slot[o_e + tok];
+#pragma unroll
+        for (int t = 0; t < kMxTiles; t++) {
+          uint16_t dv[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) dv[i] = f32_to_f16_bits(acc[t][b][i]);
+          const int row = r0 + t * 16 + g * 4;
+          uint2 v = make_uint2((uint32_t)dv[0] | ((uint32_t)dv[1] << 16),
+                               (uint32_t)dv[2] | ((uint32_t)dv[3] << 16));
+          *(uint2*)(a.d + (size_t)slot * M + row) = v;
+        }
+      }
+    }
+  }
+}
+
+// Group the T*top_k picks by expert (one workgroup). Entries of an expert keep pick order.
+struct MxGroupArgs {
+  const uint16_t* ids;  // [T*top_k]
+  int n, E;
+  int* d_expert;
+  int* d_off;
+  int* d_cnt;
+  int* nd;
+  int* ent_tok;
+  int* ent_slot;
+  uint16_t* zero;
+  int zero_len;
+  int top_k;
+};
+
+__global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
+  __shared__ int cnt[kMaxExperts];
+  __shared__ int off[kMaxExperts];
+  __shared__ int part[1024];
+  __shared__ int dpart[1024];
+  const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
+  for (int i = tid; i < a.zero_len; i += nt) a.zero[i] = 0;
+  for (int e = tid; e < a.E; e += nt) cnt[e] = 0;
+  __syncthreads();
+  // picks with an id >= E are left out (the combine skips them too)
+  for (int p = tid; p < a.n; p += nt)
+    if (a.ids[p] < a.E) atomicAdd(&cnt[a.ids[p]], 1);
+  __syncthreads();
+  // exclusive scans of counts and of "touched" over experts: thread tid owns a contiguous span
+  const int span = (a.E + nt - 1) / nt;
+  const int e0 = min(a.E, tid * span), e1 = min(a.E, e0 + span);
+  int s = 0, ds = 0;
+  for (int e = e0; e < e1; e++) {
+    s += cnt[e];
+    ds += cnt[e] > 0;
+  }
+  part[tid] = s;
+  dpart[tid] = ds;
+  __syncthreads();
+  for (int st = 1; st < nt; st <<= 1) {  // Hillis-Steele inclusive scan
+    const int v = tid >= st ? part[tid - st] : 0;
+    const int dv = tid >= st ? dpart[tid - st] : 0;
+    __syncthreads();
+    part[tid] += v;
+    dpart[tid] += dv;
+    __syncthreads();
+  }
+  int run = part[tid] - s, drun = dpart[tid] - ds;
+  for (int e = e0; e < e1; e++) {
+    off[e] = run;
+    if (cnt[e] > 0) {
+      a.d_expert[drun] = e;
+      a.d_off[drun] = run;
+      a.d_cnt[drun] = cnt[e];
+      drun++;
+    }
+    run += cnt[e];
+  }
+  if (tid == nt - 1) *a.nd = dpart[nt - 1];
+  __syncthreads();
+  // entry position = expert offset + number of earlier picks of the same expert
+  for (int p = tid; p < a.n; p += nt) {
+    const int e = a.ids[p];
+    if (e >= a.E) continue;
+    int rank = 0;
+    for (int q = 0; q < p; q++) rank += a.ids[q] == e;
+    a.ent_tok[off[e] + rank] = p / a.top_k;
+    a.ent_slot[off[e] + rank] = p;
+  }
+}
+
+// out[t][r] = bf16(sum_j w[t,j] * d[t,j][r]) in pick order (weighted_accumulate_f32).
+__global__ __launch_bounds__(256) void k_mx_combine(const uint16_t* d, const float* w,
+                                                      const uint16_t* ids, int E, uint16_t* out,
+                                                      int hidden, int top_k) {
+  const int t = (int)blockIdx.y;
+  const int r = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (r >= hidden) return;
+  float o = 0.0f;
+  for (int j = 0; j < top_k; j++) {
+    const size_t slot = (size_t)t * top_k + j;
+    if (ids[slot] >= E) continue;
+    o = add_mul_rn(o, w[slot], f16_to_f32(d[slot * hidden + r]));
+  }
+  out[(size_t)t * hidden + r] = f32_to_bf16_bits(o);
+}
+
+struct MxWs {
+  size_t d_expert, d_off, d_cnt, nd, ent_tok, ent_slot, zero, h, d, total;
+};
+
+static MxWs mx_ws(const vib3_moe_mxfp4_batch* B) {
+  MxWs w{};
+  const size_t n = (size_t)B->tokens * B->top_k;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += (bytes + 255) & ~(size_t)255;
+    return at;
+  };
+  w.d_expert = take(sizeof(int) * B->num_experts);
+  w.d_off = take(sizeof(int) * B->num_experts);
+  w.d_cnt = take(sizeof(int) * B->num_experts);
+  w.nd = take(sizeof(int));
+  w.ent_tok = take(sizeof(int) * n);
+  w.ent_slot = take(sizeof(int) * n);
+  w.zero = take(2 * (size_t)(B->hidden > B->inter ? B->hidden : B->inter));
+  w.h = take(2 * n * B->inter);
+  w.d = take(2 * n * B->hidden);
+  w.total = o;
+  return w;
+}
+
+}  // namespace vib3
+
+using namespace vib3;
+
+extern "C" {
+
+size_t vib3_moe_mxfp4_workspace_bytes(const vib3_moe_mxfp4_batch* B) {
+  if (!B || B->tokens <= 0 || B->top_k <= 0 || B->num_experts <= 0) return 0;
+  return mx_ws(B).total;
+}
+
+int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
+  if (!B) return VIB3_ERR_BAD_POINTER;
+  if (B->tokens <= 0 || B->top_k <= 0 || B->num_experts <= 0 || B->num_experts > kMaxExperts)
+    return VIB3_ERR_BAD_COUNT;
+  if ((size_t)B->tokens * B->top_k > kMxMaxPicks) return VIB3_ERR_BAD_COUNT;
+  if (B->hidden <= 0 || B->inter <= 0 || B->hidden % 256 || B->inter % 128)
+    return VIB3_ERR_UNSUPPORTED;  // 128-wide k steps; 256 rows per down workgroup
+  if (!B->x || !B->ids || !B->weights || !B->page_table || !B->out || !B->workspace)
+    return VIB3_ERR_BAD_POINTER;
+  if (((uintptr_t)B->x & 15) || ((uintptr_t)B->workspace & 255)) return VIB3_ERR_BAD_POINTER;
+  const MxWs w = mx_ws(B);
+  if (B->workspace_bytes < w.total) return VIB3_ERR_WORKSPACE;
+  char* ws = (char*)B->workspace;
+  hipStream_t st = (hipStream_t)stream;
+  const int n = B->tokens * B->top_k;
+
+  MxGroupArgs ga{};
+  ga.ids = B->ids; ga.n = n; ga.E = B->num_experts;
+  ga.d_expert = (int*)(ws + w.d_expert); ga.d_off = (int*)(ws + w.d_off);
+  ga.d_cnt = (int*)(ws + w.d_cnt); ga.nd = (int*)(ws + w.nd);
+  ga.ent_tok = (int*)(ws + w.ent_tok); ga.ent_slot = (int*)(ws + w.ent_slot);
+  ga.zero = (uint16_t*)(ws + w.zero);
+  ga.zero_len = B->hidden > B->inter ? B->hidden : B->inter;
+  ga.top_k = B->top_k;
+  hipLaunchKernelGGL(k_mx_group, dim3(1), dim3(1024), 0, st, ga);
+
+  MxArgs a{};
+  a.x = (const uint16_t*)B->x; a.table = B->page_table;
+  a.d_expert = ga.d_expert; a.d_off = ga.d_off; a.d_cnt = ga.d_cnt; a.nd = ga.nd;
+  a.ent_tok = ga.ent_tok; a.ent_slot = ga.ent_slot; a.zero = ga.zero;
+  a.h = (uint16_t*)(ws + w.h); a.d = (uint16_t*)(ws + w.d);
+  a.hidden = B->hidden; a.inter = B->inter;
+  const unsigned dmax = (unsigned)(B->num_experts < n ? B->num_experts : n);
+  hipLaunchKernelGGL(k_mx_gemm<true>, dim3(dmax, (unsigned)(B->inter / 128)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(k_mx_gemm<false>, dim3(dmax, (unsigned)(B->hidden / 256)), dim3(256), 0, st,
+                     a);
+  hipLaunchKernelGGL(k_mx_combine, dim3((unsigned)((B->hidden + 255) / 256), (unsigned)B->tokens),
+                     dim3(256), 0, st, (const uint16_t*)a.d, B->weights, B->ids,
+                     B->num_experts, (uint16_t*)B->out, B->hidden, B->top_k);
+  VIB3_RETURN_LAUNCH();
+}
+
+}  // extern "C"

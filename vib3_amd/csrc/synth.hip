@@ -76,6 +76,13 @@ __global__ void k_synth_scales(uint16_t* dst, size_t n, uint64_t seed, uint64_t 
   dst[i] = synth_scale(seed, stream, off + i, sigma, dt);
 }
 
+// E8M0 scale bytes 119 + hash % 5: 2^-8 .. 2^-4 (uniform exponent, no zero or NaN codes).
+__global__ void k_synth_e8m0(uint8_t* dst, size_t n, uint64_t seed, uint64_t stream, size_t off) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  dst[i] = (uint8_t)(119 + synth_hash(seed, stream, off + i) % 5);
+}
+
 static unsigned blocks_for(size_t n, size_t per_thread) {
   return (unsigned)((n + 256 * per_thread - 1) / (256 * per_thread));
 }
@@ -125,6 +132,24 @@ int vib3_synth_int4_page(void* page, uint64_t seed, uint64_t stream, int k, int 
   hipLaunchKernelGGL(k_synth_scales, dim3(blocks_for(ns, 1)), dim3(256), 0, s,
                      (uint16_t*)((uint8_t*)page + nd), ns, seed, stream * 2 + 1,
                      (size_t)row_start * ng, sigma, scale_dtype);
+  VIB3_RETURN_LAUNCH();
+}
+
+int vib3_synth_mxfp4_page(void* page, uint64_t seed, uint64_t stream, int k, int row_start,
+                          int rows, void* hip_stream) {
+  if (!page) return VIB3_ERR_BAD_POINTER;
+  if (k <= 0 || k % 32 || row_start < 0 || rows < 0) return VIB3_ERR_BAD_COUNT;
+  if (rows == 0) return 0;
+  hipStream_t s = (hipStream_t)hip_stream;
+  const size_t pk = (size_t)k / 2, nb = (size_t)k / 32;
+  const size_t nd = (size_t)rows * pk;
+  hipLaunchKernelGGL(k_synth_bytes, dim3(blocks_for(nd, 8)), dim3(256), 0, s, (uint8_t*)page, nd,
+                     seed, stream * 2, (size_t)row_start * pk);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  const size_t ns = (size_t)rows * nb;
+  hipLaunchKernelGGL(k_synth_e8m0, dim3(blocks_for(ns, 1)), dim3(256), 0, s,
+                     (uint8_t*)page + nd, ns, seed, stream * 2 + 1, (size_t)row_start * nb);
   VIB3_RETURN_LAUNCH();
 }
 
