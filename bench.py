@@ -38,6 +38,11 @@ CONFIGS = {
                hidden=7168, inter=2048, g=32, sdt="bf16", sigma=0.01, E=384, shared=1, k=8,
                mode=1, scaling=2.827, router_sigma=0.01, bias_sigma=0.1, x_dtype="bf16",
                layout="paged", seed=0x5EED0003, layers=4),
+    "c4": dict(workload="c4: batched decode, 64 tokens bf16, top-8 Zipf(1.1) over 384 MXFP4 experts "
+                        "(Kimi-K2.5 shape: hidden 7168, inter 2048; e2m1 codes, e8m0 per 32), "
+                        "grouped per expert as a grouped GEMM on MFMA with fused SwiGLU, bf16 out",
+               hidden=7168, inter=2048, E=384, k=8, tokens=64, zipf=1.1, seed=0x5EED0004,
+               layers=2, batches=8),
     "c1": dict(workload="c1: Mixtral-8x7B MoE layer decode, batch 1 (router fp32 [8,4096] softmax "
                         "top-2; 8 INT4 experts 14336x4096, g128 fp16 scales; x fp16)",
                hidden=4096, inter=14336, g=128, sdt="f16", sigma=0.02, E=8, shared=0, k=2,
@@ -103,6 +108,110 @@ def cpu_baseline(cfg, bank, w, b, x, ids, wts, budget_s: float):
             "reps": len(times)}
 
 
+def bench_c4(args, cfg) -> int:
+    """c4: batched MXFP4 decode. A step = one batch of 64 tokens through the MoE sublayer."""
+    import numpy as np
+    import torch
+
+    from vib3_amd import _hip, _lib, mxfp4
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream(dev).cuda_stream
+    H, I, E, K, T = cfg["hidden"], cfg["inter"], cfg["E"], cfg["k"], cfg["tokens"]
+    L = args.layers or cfg["layers"]
+    t0 = time.perf_counter()
+    banks = []
+    for l in range(L):
+        banks.append(mxfp4.Mxfp4ExpertBank(H, I, E, layer=l, seed=cfg["seed"], device=dev))
+        torch.cuda.synchronize()
+        log(f"[bench] layer {l} ready ({banks[-1].nbytes / 1e9:.2f} GB, {time.perf_counter() - t0:.1f}s)")
+    nb = cfg["batches"]
+    picks = [mxfp4.zipf_picks(T, E, K, s=cfg["zipf"], seed=cfg["seed"] + b) for b in range(nb)]
+    xs = []
+    for b in range(nb):
+        x = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+        _lib.call("vib3_synth_normal", x.data_ptr(), 2, T * H, cfg["seed"], 1000 + b, 0, 1.0, st)
+        xs.append(x)
+    dev_picks = [(torch.from_numpy(i.view(np.int16)).to(dev), torch.from_numpy(w).to(dev))
+                 for i, w in picks]
+    runners = [mxfp4.MoeMxfp4Batch(bk, T, K) for bk in banks]
+    descs = [[r.desc(xs[b], *dev_picks[b]) for b in range(nb)] for r in runners]
+    launch = _lib.load().vib3_launch_moe_mxfp4_batched
+
+    def step(i):
+        rc = launch(descs[i % L][i % nb], st)
+        if rc:
+            raise _lib.Vib3Error("vib3_launch_moe_mxfp4_batched", rc)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = _hip.Event(), _hip.Event()
+    e0.record(st)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    e1.record(st)
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) * 1e3 / args.steps
+
+    # algorithmic bytes: every touched expert's three pages once, activations in, output out
+    ebytes = banks[0].expert_bytes
+    distinct = [len(np.unique(i)) for i, _ in picks]
+    avg_bytes = float(np.mean(distinct)) * ebytes + 2 * T * H * 2
+    flops = T * K * 3 * 2 * H * I
+    gbs = avg_bytes / (us * 1e-6) / 1e9
+    log(f"[bench] {args.steps} batches: {us:.1f} us/batch, {np.mean(distinct):.1f} experts/batch, "
+        f"{gbs:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        ids, w = picks[0]
+        sample = [0, 1]
+        xh = O.to_f32(xs[0].view(torch.int16).cpu().numpy().view(np.uint16).ravel(),
+                      O.BF16).reshape(T, H)
+        used = sorted({int(e) for e in ids[sample].ravel()})
+        empty = np.zeros(1, dtype=np.uint8)
+        pages = [banks[0].expert_pages_host(e) if e in used else (empty, empty, empty)
+                 for e in range(E)]
+        threads = min(16, os.cpu_count() or 1)
+        O.moe_mxfp4_batched(xh[sample], H, I, pages, ids[sample], w[sample], nthreads=threads)
+        times = []
+        t_end = time.perf_counter() + args.cpu_seconds
+        while time.perf_counter() < t_end or len(times) < 2:
+            c0 = time.perf_counter()
+            O.moe_mxfp4_batched(xh[sample], H, I, pages, ids[sample], w[sample], nthreads=threads)
+            times.append(time.perf_counter() - c0)
+        per_tok = statistics.median(times) / len(sample)
+        cpu = {"value": round(per_tok * T * 1e6, 1), "unit": "us/batch", "cores": threads,
+               "kind": "port",
+               "sample": f"c-oracle per-token restatement on {len(sample)} tokens of batch 0 "
+                         f"(8 experts each), median of {len(times)} reps, scaled x{T // len(sample)} "
+                         f"to the 64-token batch"}
+
+    out = {
+        "metric": "MoE batched decode us per 64-token batch (Kimi-K2.5 shape, MXFP4 experts)",
+        "value": round(us, 2), "unit": "us/batch", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us / 1e3, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "mxfp4 weights x bf16 activations, bf16/f16 MFMA, f32 accumulate",
+        "data": "synthetic (counter-based generator; random-init weights of the named shape)",
+        "config": {"workload": cfg["workload"], "layers_rotated": L, "batches": nb,
+                   "distinct_experts_per_batch": round(float(np.mean(distinct)), 1),
+                   "algorithmic_bytes_per_batch": round(avg_bytes)},
+        "roofline": {"bound": "hbm", "kernel": "k_mx_gemm (gate/up + down grouped GEMM, whole batch)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "mfma": {"achieved_tflops": round(flops / (us * 1e-6) / 1e12, 2), "peak_tflops_bf16": 2500.0,
+                 "frac": round(flops / (us * 1e-6) / 2.5e15, 5)},
+        "tokens_per_s": round(T / (us * 1e-6)),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -130,6 +239,8 @@ def main() -> int:
     from vib3_amd._lib import DT_BF16, DT_F16, DT_F32
 
     cfg = dict(CONFIGS[args.config])
+    if args.config == "c4":
+        return bench_c4(args, cfg)
     if args.layers:
         cfg["layers"] = args.layers
     torch.cuda.set_device(0)

@@ -194,7 +194,7 @@ typedef struct vib3_moe_mxfp4_batch {
     const void *x;           /* [tokens][hidden] bf16, 16-byte aligned */
     int tokens;
     int hidden;              /* multiple of 256 */
-    int inter;               /* multiple of 128 */
+    int inter;               /* multiple of 256 */
     int num_experts;         /* <= 4096 */
     int top_k;               /* tokens * top_k <= 4096 */
     const uint16_t *ids;     /* [tokens][top_k] device; ids >= num_experts are skipped */

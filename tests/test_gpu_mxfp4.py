@@ -81,11 +81,11 @@ def test_synth_mxfp4_page_device_matches_oracle():
     assert np.array_equal(buf.cpu().numpy(), O.synth_mxfp4_page(SEED, 31, k, 8, rows))
 
 
-@pytest.mark.parametrize("hidden,inter,E,T,k", [(256, 128, 12, 5, 3), (512, 384, 9, 37, 4),
+@pytest.mark.parametrize("hidden,inter,E,T,k", [(256, 256, 12, 5, 3), (512, 768, 9, 37, 4),
                                                  (256, 256, 3, 70, 2)])
 def test_small_batches_match_oracle(hidden, inter, E, T, k):
-    """Shapes with 1..70 tokens per expert (several 16-token column blocks, a second 64-token
-    pass), experts picked twice by one token, and experts never picked."""
+    """Shapes with 1..70 tokens per expert (several 16-token passes), experts picked twice by
+    one token, and experts never picked."""
     _say(f"[mxfp4] small hidden={hidden} inter={inter} E={E} T={T} k={k}")
     from vib3_amd.mxfp4 import zipf_picks
     bank = _bank(hidden, inter, E)
@@ -101,7 +101,7 @@ def test_small_batches_match_oracle(hidden, inter, E, T, k):
 
 def test_out_of_range_ids_are_skipped():
     _say("[mxfp4] out-of-range ids")
-    hidden, inter, E, T, k = 256, 128, 5, 4, 3
+    hidden, inter, E, T, k = 256, 256, 5, 4, 3
     bank = _bank(hidden, inter, E)
     ids = np.array([[0, 1, 2], [E, 3, 4], [4, 4000, 1], [E + 7, E, E]], dtype=np.uint16)
     w = np.full((T, k), 0.5, dtype=np.float32)
@@ -133,7 +133,7 @@ def test_kimi_shape_batch_zipf():
 def test_argument_errors():
     from vib3_amd import _lib
     from vib3_amd.mxfp4 import MoeMxfp4Batch
-    bank = _bank(256, 128, 4)
+    bank = _bank(256, 256, 4)
     b = MoeMxfp4Batch(bank, 2, 2)
     x, _ = _x(2, 256)
     ids = torch.zeros((2, 2), dtype=torch.int16, device="cuda")

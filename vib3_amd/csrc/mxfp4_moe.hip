@@ -31,8 +31,8 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMxTokBlk = 16;            // tokens per MFMA column block
-constexpr int kMxMaxBlk = 4;             // column blocks per pass (64 tokens)
-constexpr int kMxStep = 128;             // k per step: 4 lane groups x 32
+constexpr int kMxMaxBlk = 1;             // column blocks per pass (16 tokens; more = more passes)
+constexpr int kMxStep = 256;             // k per step: 2 halves x 4 lane groups x 32
 constexpr int kMxTiles = 4;              // 16-row A tiles per wave
 constexpr int kMxMaxPicks = 4096;        // tokens * top_k per launch (grouping is one workgroup)
 
@@ -43,6 +43,9 @@ struct MxArgs {
   const int* d_off;           // [nd] first entry of d
   const int* d_cnt;           // [nd] entries of d
   const int* nd;              // number of distinct experts
+  const int* it_d;            // [items] distinct index of each work item
+  const int* it_p0;           // [items] first entry of the item within its expert
+  const int* nitems;
   const int* ent_tok;         // [T*top_k] token of each entry (grouped by expert)
   const int* ent_slot;        // [T*top_k] t*top_k + j of each entry
   const uint16_t* zero;       // zero row (>= max(hidden, inter) halves)
@@ -82,7 +85,7 @@ __device__ __forceinline__ void decode8(uint32_t w, float scale, bf16x8_t& ob, f
   }
 }
 
-// One wave: kMxTiles tiles of 16 weight rows x all the expert's tokens (in passes of 64).
+// One wave: kMxTiles tiles of 16 weight rows x all the expert's tokens (in passes of 16).
 // GATEUP: tiles 0,1 = up rows r0..r0+31, tiles 2,3 = gate rows r0..r0+31 (bf16 MFMA on x);
 // otherwise tiles 0..3 = down rows r0..r0+63 (f16 MFMA on h).
 //
@@ -92,18 +95,92 @@ __device__ __forceinline__ void decode8(uint32_t w, float scale, bf16x8_t& ob, f
 // four k blocks of one MFMA are then k = step*128 + g*32 + s*8 (g = lane group), a fixed
 // permutation of the step's k range that A and B share. The scale of the whole 32-code chunk
 // is one E8M0 byte. Result D: lane l holds rows (l >> 4)*4 + i, column l & 15.
+
+template <int NB>
+struct MxStep {
+  uint4 w[kMxTiles][2];
+  uint8_t sc[kMxTiles][2];
+  uint4 xb[NB][2][4];
+};
+
+// One pass over k for NB column blocks; loads run one step ahead of the matrix-core work.
+// A step is 256 k: the lane's 16 bytes at k = ks + g*32 (half 0) and ks + 128 + g*32 (half 1),
+// so the four lanes of a row fetch both 64-byte halves of its 128-byte line together.
+template <bool GATEUP, int NB>
+__device__ __forceinline__ void mx_pass(const uint8_t* const (&tcode)[kMxTiles],
+                                        const uint8_t* const (&tscale)[kMxTiles],
+                                        const uint16_t* const (&brow)[kMxMaxBlk], int K,
+                                        f32x4_t (&acc)[kMxTiles][kMxMaxBlk]) {
+  auto load = [&](MxStep<NB>& st, int ks) {
+#pragma unroll
+    for (int t = 0; t < kMxTiles; t++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        st.w[t][h] = ld16(tcode[t] + ks / 2 + h * 64);
+        st.sc[t][h] = ld_u8(tscale[t] + ks / 32 + h * 4);
+      }
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int s = 0; s < 4; s++) st.xb[b][h][s] = ld16(brow[b] + ks + h * 128 + s * 8);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto compute = [&](const MxStep<NB>& st) {
+#pragma unroll
+    for (int t = 0; t < kMxTiles; t++) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const float scale = e8m0_scale(st.sc[t][h]);
+        const uint32_t words[4] = {st.w[t][h].x, st.w[t][h].y, st.w[t][h].z, st.w[t][h].w};
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+          bf16x8_t ab;
+          f16x8_t ah;
+          decode8<GATEUP>(words[s], scale, ab, ah);
+#pragma unroll
+          for (int b = 0; b < NB; b++) {
+            if (GATEUP) {
+              acc[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  ab, __builtin_bit_cast(bf16x8_t, st.xb[b][h][s]), acc[t][b], 0, 0, 0);
+            } else {
+              acc[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                  ah, __builtin_bit_cast(f16x8_t, st.xb[b][h][s]), acc[t][b], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+  };
+  MxStep<NB> A, B;
+  const int last = K - kMxStep;
+  load(A, 0);
+  for (int ks = 0;; ks += 2 * kMxStep) {
+    load(B, min(ks + kMxStep, last));  // past the end: re-reads the last step (no branch)
+    compute(A);
+    if (ks + kMxStep >= K) break;
+    load(A, min(ks + 2 * kMxStep, last));
+    compute(B);
+    if (ks + 2 * kMxStep >= K) break;
+  }
+}
+
 template <bool GATEUP>
 __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
-  const int dix = (int)blockIdx.x;
-  if (dix >= *a.nd) return;
+  // work item = (distinct expert, 16-token slice); blockIdx.x = row block of the item
+  const int item = (int)blockIdx.y;
+  if (item >= *a.nitems) return;
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int rr = lane & 15, g = lane >> 4;
+  const int dix = a.it_d[item];
   const int e = a.d_expert[dix], o_e = a.d_off[dix], t_e = a.d_cnt[dix];
+  const int p0 = a.it_p0[item];
   const int K = GATEUP ? a.hidden : a.inter;   // reduction
   const int M = GATEUP ? a.inter : a.hidden;   // rows of each matrix
   const int rows_per_wave = GATEUP ? 32 : 64;
-  const int r0 = ((int)blockIdx.y * 4 + wave) * rows_per_wave;
+  const int r0 = ((int)blockIdx.x * 4 + wave) * rows_per_wave;
   if (r0 >= M) return;
   const size_t pkb = (size_t)K / 2, nsb = (size_t)K / 32;
   const uint8_t* m0 = (const uint8_t*)a.table[(size_t)e * 3 + (GATEUP ? 0 : 2)];
@@ -120,15 +197,15 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
     tscale[t] = base + (size_t)M * pkb + (size_t)row * nsb + g;
   }
 
-  for (int p0 = 0; p0 < t_e; p0 += kMxTokBlk * kMxMaxBlk) {
-    const int nblk = min(kMxMaxBlk, (t_e - p0 + kMxTokBlk - 1) / kMxTokBlk);
+  {
+    const int nblk = 1;
     // B rows of this lane's column in each block (zero row past the expert's tokens)
     const uint16_t* brow[kMxMaxBlk];
 #pragma unroll
     for (int b = 0; b < kMxMaxBlk; b++) {
       const int tok = p0 + b * kMxTokBlk + rr;
       const uint16_t* r = a.zero;
-      if (b < nblk && tok < t_e) {
+      if (tok < t_e) {
         r = GATEUP ? a.x + (size_t)a.ent_tok[o_e + tok] * K : a.h + (size_t)(o_e + tok) * K;
       }
       brow[b] = r + g * 32;
@@ -138,47 +215,7 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
     for (int t = 0; t < kMxTiles; t++)
 #pragma unroll
       for (int b = 0; b < kMxMaxBlk; b++) acc[t][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    for (int ks = 0; ks < K; ks += kMxStep) {
-      uint4 w[kMxTiles];
-      uint8_t sc[kMxTiles];
-#pragma unroll
-      for (int t = 0; t < kMxTiles; t++) {
-        w[t] = ld16(tcode[t] + ks / 2);
-        sc[t] = ld_u8(tscale[t] + ks / 32);
-      }
-      uint4 xb[kMxMaxBlk][4];
-#pragma unroll
-      for (int b = 0; b < kMxMaxBlk; b++) {
-        if (b < nblk) {
-#pragma unroll
-          for (int s = 0; s < 4; s++) xb[b][s] = ld16(brow[b] + ks + s * 8);
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < kMxTiles; t++) {
-        const float scale = e8m0_scale(sc[t]);
-        const uint32_t words[4] = {w[t].x, w[t].y, w[t].z, w[t].w};
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-          bf16x8_t ab;
-          f16x8_t ah;
-          decode8<GATEUP>(words[s], scale, ab, ah);
-#pragma unroll
-          for (int b = 0; b < kMxMaxBlk; b++) {
-            if (b < nblk) {
-              if (GATEUP) {
-                acc[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    ab, __builtin_bit_cast(bf16x8_t, xb[b][s]), acc[t][b], 0, 0, 0);
-              } else {
-                acc[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    ah, __builtin_bit_cast(f16x8_t, xb[b][s]), acc[t][b], 0, 0, 0);
-              }
-            }
-          }
-        }
-      }
-    }
+    mx_pass<GATEUP, kMxMaxBlk>(tcode, tscale, brow, K, acc);
 
     // epilogue: lane holds rows (g*4 + i) of each tile for token column rr of each block
 #pragma unroll
@@ -217,6 +254,7 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
 }
 
 // Group the T*top_k picks by expert (one workgroup). Entries of an expert keep pick order.
+// Work items for the GEMM kernels are (distinct expert, 16-token slice of its entries).
 struct MxGroupArgs {
   const uint16_t* ids;  // [T*top_k]
   int n, E;
@@ -224,6 +262,9 @@ struct MxGroupArgs {
   int* d_off;
   int* d_cnt;
   int* nd;
+  int* it_d;            // [items] distinct index of each work item
+  int* it_p0;           // [items] first entry (within the expert) of each work item
+  int* nitems;
   int* ent_tok;
   int* ent_slot;
   uint16_t* zero;
@@ -234,54 +275,68 @@ struct MxGroupArgs {
 __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int off[kMaxExperts];
-  __shared__ int part[1024];
-  __shared__ int dpart[1024];
+  __shared__ int part[1024], dpart[1024], ipart[1024];
+  __shared__ uint16_t sid[kMxMaxPicks];
   const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
   for (int i = tid; i < a.zero_len; i += nt) a.zero[i] = 0;
   for (int e = tid; e < a.E; e += nt) cnt[e] = 0;
+  for (int p = tid; p < a.n; p += nt) sid[p] = a.ids[p];
   __syncthreads();
   // picks with an id >= E are left out (the combine skips them too)
   for (int p = tid; p < a.n; p += nt)
-    if (a.ids[p] < a.E) atomicAdd(&cnt[a.ids[p]], 1);
+    if (sid[p] < a.E) atomicAdd(&cnt[sid[p]], 1);
   __syncthreads();
-  // exclusive scans of counts and of "touched" over experts: thread tid owns a contiguous span
+  // exclusive scans over experts of: entries, touched experts, work items. Thread tid owns a
+  // contiguous span of experts.
   const int span = (a.E + nt - 1) / nt;
   const int e0 = min(a.E, tid * span), e1 = min(a.E, e0 + span);
-  int s = 0, ds = 0;
+  int s = 0, ds = 0, is = 0;
   for (int e = e0; e < e1; e++) {
     s += cnt[e];
     ds += cnt[e] > 0;
+    is += (cnt[e] + kMxTokBlk - 1) / kMxTokBlk;
   }
   part[tid] = s;
   dpart[tid] = ds;
+  ipart[tid] = is;
   __syncthreads();
-  for (int st = 1; st < nt; st <<= 1) {  // Hillis-Steele inclusive scan
+  for (int st = 1; st < nt; st <<= 1) {  // Hillis-Steele inclusive scans
     const int v = tid >= st ? part[tid - st] : 0;
     const int dv = tid >= st ? dpart[tid - st] : 0;
+    const int iv = tid >= st ? ipart[tid - st] : 0;
     __syncthreads();
     part[tid] += v;
     dpart[tid] += dv;
+    ipart[tid] += iv;
     __syncthreads();
   }
-  int run = part[tid] - s, drun = dpart[tid] - ds;
+  int run = part[tid] - s, drun = dpart[tid] - ds, irun = ipart[tid] - is;
   for (int e = e0; e < e1; e++) {
     off[e] = run;
     if (cnt[e] > 0) {
       a.d_expert[drun] = e;
       a.d_off[drun] = run;
       a.d_cnt[drun] = cnt[e];
+      for (int p0 = 0; p0 < cnt[e]; p0 += kMxTokBlk) {
+        a.it_d[irun] = drun;
+        a.it_p0[irun] = p0;
+        irun++;
+      }
       drun++;
     }
     run += cnt[e];
   }
-  if (tid == nt - 1) *a.nd = dpart[nt - 1];
+  if (tid == nt - 1) {
+    *a.nd = dpart[nt - 1];
+    *a.nitems = ipart[nt - 1];
+  }
   __syncthreads();
   // entry position = expert offset + number of earlier picks of the same expert
   for (int p = tid; p < a.n; p += nt) {
-    const int e = a.ids[p];
+    const int e = sid[p];
     if (e >= a.E) continue;
     int rank = 0;
-    for (int q = 0; q < p; q++) rank += a.ids[q] == e;
+    for (int q = 0; q < p; q++) rank += sid[q] == e;
     a.ent_tok[off[e] + rank] = p / a.top_k;
     a.ent_slot[off[e] + rank] = p;
   }
@@ -304,8 +359,14 @@ __global__ __launch_bounds__(256) void k_mx_combine(const uint16_t* d, const flo
 }
 
 struct MxWs {
-  size_t d_expert, d_off, d_cnt, nd, ent_tok, ent_slot, zero, h, d, total;
+  size_t d_expert, d_off, d_cnt, nd, it_d, it_p0, nitems, ent_tok, ent_slot, zero, h, d, total;
 };
+
+// Upper bound of the work items: sum over touched experts of ceil(count / 16).
+static int mx_max_items(const vib3_moe_mxfp4_batch* B) {
+  const int n = B->tokens * B->top_k;
+  return n / kMxTokBlk + (B->num_experts < n ? B->num_experts : n);
+}
 
 static MxWs mx_ws(const vib3_moe_mxfp4_batch* B) {
   MxWs w{};
@@ -320,6 +381,9 @@ static MxWs mx_ws(const vib3_moe_mxfp4_batch* B) {
   w.d_off = take(sizeof(int) * B->num_experts);
   w.d_cnt = take(sizeof(int) * B->num_experts);
   w.nd = take(sizeof(int));
+  w.it_d = take(sizeof(int) * (size_t)mx_max_items(B));
+  w.it_p0 = take(sizeof(int) * (size_t)mx_max_items(B));
+  w.nitems = take(sizeof(int));
   w.ent_tok = take(sizeof(int) * n);
   w.ent_slot = take(sizeof(int) * n);
   w.zero = take(2 * (size_t)(B->hidden > B->inter ? B->hidden : B->inter));
@@ -345,8 +409,8 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   if (B->tokens <= 0 || B->top_k <= 0 || B->num_experts <= 0 || B->num_experts > kMaxExperts)
     return VIB3_ERR_BAD_COUNT;
   if ((size_t)B->tokens * B->top_k > kMxMaxPicks) return VIB3_ERR_BAD_COUNT;
-  if (B->hidden <= 0 || B->inter <= 0 || B->hidden % 256 || B->inter % 128)
-    return VIB3_ERR_UNSUPPORTED;  // 128-wide k steps; 256 rows per down workgroup
+  if (B->hidden <= 0 || B->inter <= 0 || B->hidden % 256 || B->inter % 256)
+    return VIB3_ERR_UNSUPPORTED;  // 256-wide k steps; 256 rows per down workgroup
   if (!B->x || !B->ids || !B->weights || !B->page_table || !B->out || !B->workspace)
     return VIB3_ERR_BAD_POINTER;
   if (((uintptr_t)B->x & 15) || ((uintptr_t)B->workspace & 255)) return VIB3_ERR_BAD_POINTER;
@@ -361,6 +425,7 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   ga.d_expert = (int*)(ws + w.d_expert); ga.d_off = (int*)(ws + w.d_off);
   ga.d_cnt = (int*)(ws + w.d_cnt); ga.nd = (int*)(ws + w.nd);
   ga.ent_tok = (int*)(ws + w.ent_tok); ga.ent_slot = (int*)(ws + w.ent_slot);
+  ga.it_d = (int*)(ws + w.it_d); ga.it_p0 = (int*)(ws + w.it_p0); ga.nitems = (int*)(ws + w.nitems);
   ga.zero = (uint16_t*)(ws + w.zero);
   ga.zero_len = B->hidden > B->inter ? B->hidden : B->inter;
   ga.top_k = B->top_k;
@@ -369,12 +434,13 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   MxArgs a{};
   a.x = (const uint16_t*)B->x; a.table = B->page_table;
   a.d_expert = ga.d_expert; a.d_off = ga.d_off; a.d_cnt = ga.d_cnt; a.nd = ga.nd;
+  a.it_d = ga.it_d; a.it_p0 = ga.it_p0; a.nitems = ga.nitems;
   a.ent_tok = ga.ent_tok; a.ent_slot = ga.ent_slot; a.zero = ga.zero;
   a.h = (uint16_t*)(ws + w.h); a.d = (uint16_t*)(ws + w.d);
   a.hidden = B->hidden; a.inter = B->inter;
-  const unsigned dmax = (unsigned)(B->num_experts < n ? B->num_experts : n);
-  hipLaunchKernelGGL(k_mx_gemm<true>, dim3(dmax, (unsigned)(B->inter / 128)), dim3(256), 0, st, a);
-  hipLaunchKernelGGL(k_mx_gemm<false>, dim3(dmax, (unsigned)(B->hidden / 256)), dim3(256), 0, st,
+  const unsigned items = (unsigned)mx_max_items(B);
+  hipLaunchKernelGGL(k_mx_gemm<true>, dim3((unsigned)(B->inter / 128), items), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(k_mx_gemm<false>, dim3((unsigned)(B->hidden / 256), items), dim3(256), 0, st,
                      a);
   hipLaunchKernelGGL(k_mx_combine, dim3((unsigned)((B->hidden + 255) / 256), (unsigned)B->tokens),
                      dim3(256), 0, st, (const uint16_t*)a.d, B->weights, B->ids,
