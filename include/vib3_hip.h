@@ -173,7 +173,13 @@ typedef struct vib3_moe_int4_layer {
     size_t workspace_bytes;
 } vib3_moe_int4_layer;
 
+/* Workspace bytes for `layer`. Zero a new workspace once before its first launch
+ * (vib3_hip_zero): the router publishes logits there under per-launch tags, and 0 is never a tag. */
 size_t vib3_moe_int4_workspace_bytes(const vib3_moe_int4_layer *layer);
+
+/* 1 when the layer computes the router logits and top-k inside its gate/up kernel (up to 512
+ * experts), 0 when the router runs as launches of its own. */
+int vib3_moe_int4_router_fused(const vib3_moe_int4_layer *layer);
 int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer *layer, void *stream);
 
 /* One stage of the same layer: 0 = router (logits and, when separate, selection), 1 = fused

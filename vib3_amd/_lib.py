@@ -74,6 +74,7 @@ SIGNATURES = {
     "vib3_launch_router_topk_ex": (I, [P, I, P, I, P, I, I, I, I, F, I, P, P, P, P, P]),
     "vib3_moe_int4_workspace_bytes": (S, [C.POINTER(MoeInt4Layer)]),
     "vib3_launch_moe_int4_layer": (I, [C.POINTER(MoeInt4Layer), P]),
+    "vib3_moe_int4_router_fused": (I, [C.POINTER(MoeInt4Layer)]),
     "vib3_launch_moe_int4_layer_stage": (I, [C.POINTER(MoeInt4Layer), I, P]),
     "vib3_moe_mxfp4_workspace_bytes": (S, [C.POINTER(MoeMxfp4Batch)]),
     "vib3_launch_moe_mxfp4_batched": (I, [C.POINTER(MoeMxfp4Batch), P]),

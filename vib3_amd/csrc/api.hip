@@ -3,6 +3,8 @@
 // nothing and keep no mutable global state, so they are reentrant across streams.
 #include <string.h>
 
+#include <atomic>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -67,8 +69,27 @@ __global__ void k_zero(uint4* p16, size_t n16, uint8_t* tail, size_t ntail) {
 
 // Workspace of the fused layer: [scores[E] | ids[k] | wts[k] | h[nslots][inter]].
 struct LayerWs {
-  size_t scores, ids, wts, h, total;
+  size_t scores, ids, wts, slots, error, h, total;
 };
+
+// Routing mode of a layer call (see RowsArgs::route).
+int router_mode(const vib3_moe_int4_layer* L) {
+  if (!L->router_w || L->top_k <= 0) return kRouteGiven;
+  int mode = L->num_experts <= kMaxExpertsInKernel ? 2 : 0;
+  if (const char* v = getenv("VIB3_ROUTE_MODE")) {
+    const int m = atoi(v);
+    if (m >= 0 && m <= 2) mode = L->num_experts <= kMaxExpertsInKernel ? m : 0;
+  }
+  return mode == 2 ? kRouteFused : mode == 1 ? kRouteScores : kRouteGiven;
+}
+
+// Tag of a launch's router slots: process-wide counter, never 0 (a zeroed workspace holds 0).
+uint32_t next_generation() {
+  static std::atomic<uint32_t> gen{0};
+  uint32_t g = gen.fetch_add(1, std::memory_order_relaxed) + 1;
+  if (g == 0) g = gen.fetch_add(1, std::memory_order_relaxed) + 1;
+  return g;
+}
 
 LayerWs layer_ws(const vib3_moe_int4_layer* L) {
   LayerWs w{};
@@ -77,7 +98,9 @@ LayerWs layer_ws(const vib3_moe_int4_layer* L) {
   w.scores = 0;
   w.ids = round_up(w.scores + 4 * (size_t)(L->num_experts > 0 ? L->num_experts : 0), 256);
   w.wts = round_up(w.ids + 2 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
-  w.h = round_up(w.wts + 4 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
+  w.slots = round_up(w.wts + 4 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
+  w.error = round_up(w.slots + 8 * (size_t)(L->num_experts > 0 ? L->num_experts : 0), 256);
+  w.h = round_up(w.error + 4, 256);
   w.total = round_up(w.h + hsz * (size_t)(nslots > 0 ? nslots : 0) * (size_t)(L->inter > 0 ? L->inter : 0), 256);
   return w;
 }
@@ -281,7 +304,7 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
   const uint16_t* ids = (const uint16_t*)(ws + w.ids);
   const float* wts = (const float*)(ws + w.wts);
   RouterArgs router{};
-  bool route_in_kernel = false;
+  int route = kRouteGiven;
   if (L->top_k > 0) {
     if (L->router_w) {
       if (!valid_act_dt(L->router_w_dtype)) return VIB3_ERR_UNSUPPORTED;
@@ -299,13 +322,18 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
       router.wts = (float*)(ws + w.wts);
       router.out_ids = L->out_ids;
       router.out_wts = L->out_weights;
-      // small expert counts select inside the gate/up kernel; larger ones need a launch
-      route_in_kernel = L->num_experts <= kMaxExpertsInKernel && L->hidden <= 256 * 32;
-      if (const char* v = getenv("VIB3_ROUTE_IN_KERNEL")) route_in_kernel &= atoi(v) != 0;
-      if (run(0)) {
+      // up to 512 experts: logits and selection inside the gate/up kernel (fused); larger
+      // counts: the router kernel plus a selection launch. VIB3_ROUTE_MODE (tuning/diagnosis)
+      // forces 0 = separate selection launch, 1 = selection in the gate/up prologue from the
+      // router kernel's scores, 2 = fused.
+      route = router_mode(L);
+      router.slots = (uint64_t*)(ws + w.slots);
+      router.error = (int*)(ws + w.error);
+      router.gen = next_generation();
+      if (run(0) && route != kRouteFused) {
         int rc = launch_router_logits(router, st);
         if (rc) return rc;
-        if (!route_in_kernel) {
+        if (route == kRouteGiven) {  // selection kernel publishes ids / weights
           rc = launch_router_select(router, st);
           if (rc) return rc;
         }
@@ -328,7 +356,7 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
     a.magic[q] = page_magic(L->rows_per_page[q]);
   }
   a.out = ws + w.h; a.out_dt = h_dt; a.out_stride = (size_t)L->inter;
-  a.route = route_in_kernel;
+  a.route = route;
   a.router = router;
   if (run(1)) {
     int rc = launch_rows(a, true, st);
@@ -348,6 +376,10 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
 
 int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
   return moe_int4_layer(L, stream, -1);
+}
+
+int vib3_moe_int4_router_fused(const vib3_moe_int4_layer* L) {
+  return L && router_mode(L) == kRouteFused ? 1 : 0;
 }
 
 int vib3_launch_moe_int4_layer_stage(const vib3_moe_int4_layer* L, int stage, void* stream) {

@@ -77,6 +77,11 @@ __device__ __forceinline__ float add_mul_rn(float o, float w, float d) {
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
+// Wait for this wave's LDS (and scalar memory) operations only: s_waitcnt lgkmcnt(0) with the
+// vector-memory and export counters left at their maximum, so loads still in flight (streamed
+// weights issued ahead of time) are not drained.
+__device__ __forceinline__ void wait_lgkm() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 // ------------------------------------------------------------------------- INT4 chunk dot
 //
 // A chunk is 16 bytes of one weight row = 32 consecutive columns. Word i of the chunk holds
@@ -247,6 +252,27 @@ __device__ __forceinline__ void mat_row(const MatRef& m, int r, int pk, int ng, 
 }
 
 }  // namespace vib3
+
+// Timeline probes for kernel-internal phases: compiled in only when VIB3_TRACE is defined (a
+// profiling build that also defines `uint64_t* vib3_trace_buf` in device memory); each probe
+// stores the 100 MHz real-time counter for (workgroup, point).
+#ifdef VIB3_TRACE
+#define VIB3_TRACE_POINT(k)                                                          \
+  do {                                                                               \
+    if (threadIdx.x == 0) vib3_trace_buf[blockIdx.x * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#define VIB3_TRACE_VALUE(k, v)                                                       \
+  do {                                                                               \
+    if (threadIdx.x == 0) vib3_trace_buf[blockIdx.x * 16 + (k)] = (uint64_t)(v);       \
+  } while (0)
+#else
+#define VIB3_TRACE_VALUE(k, v) \
+  do {                         \
+  } while (0)
+#define VIB3_TRACE_POINT(k) \
+  do {                      \
+  } while (0)
+#endif
 
 // Launch-error plumbing shared by the launchers.
 #define VIB3_RETURN_LAUNCH()                      \

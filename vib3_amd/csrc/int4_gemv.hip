@@ -17,6 +17,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "router_dot.h"
 #include "select.h"
 
 namespace vib3 {
@@ -162,6 +163,7 @@ constexpr int kRowsBuffers = VIB3_ROWS_BUFFERS;
 
 template <int NCH, bool DUAL, bool SPLIT, bool PAGED>
 __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
+  VIB3_TRACE_POINT(0);
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform (SGPR)
   const int pk = a.K / 2, ng = (a.K + a.g - 1) / a.g, cpr = a.K / 32;
@@ -256,22 +258,56 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   }
   // a shared-expert row needs no routing: start its loads before the selection
   const bool early = have && PAGED && slot_of(it0 / M) >= top_k;
-  if (early) start(buf[0], 0, true, it0);
+  // Fused routing: workgroup b computes router rows b, b + grid, ... and publishes each as a
+  // tagged slot. The first row's loads go out before the shared-expert row's, so the router,
+  // which every routed row waits for, is not queued behind the expert stream.
+  const bool fused = PAGED && a.route == kRouteFused;
+  const bool split_row = fused && (int)blockIdx.x < a.router.E && router_row_splittable(a.router);
+  RouterRowRaw rrow;
+  if (split_row) router_row_issue(a.router, (int)blockIdx.x, rrow);
+  // a workgroup computing a router row starts its expert stream only after the selection: the
+  // CU's memory pipeline then serves the router rows, which every workgroup waits for, first
+  const bool early_now = early && !(fused && (int)blockIdx.x < a.router.E);
+  if (early_now) start(buf[0], 0, true, it0);
+  if (fused) {
+    auto publish = [&](int e, float sc) {
+      if (threadIdx.x == 0) {
+        __hip_atomic_store(a.router.slots + e,
+                           ((uint64_t)a.router.gen << 32) | __float_as_uint(sc), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        if (a.router.scores) a.router.scores[e] = sc;
+      }
+    };
+    int e = (int)blockIdx.x;
+    if (split_row) {
+      publish(e, router_row_finish(a.router, rrow));
+      e += (int)gridDim.x;
+    }
+    for (; e < a.router.E; e += (int)gridDim.x) {
+      publish(e, router_row_dot(a.router, e));
+      __syncthreads();  // router_row_dot's reduction buffer is reused by the next row
+    }
+  }
+  VIB3_TRACE_POINT(1);
   if (PAGED && top_k > 0 && wave == 0) {
-    if (a.route) {
+    if (a.route == kRouteFused) {
+      select_topk_published_small(a.router, s_sel, s_wts, blockIdx.x == 0);
+    } else if (a.route == kRouteScores) {
       select_topk_small(a.router, a.router.scores, s_sel, s_wts, blockIdx.x == 0);
     } else if (lane < top_k) {
       s_sel[lane] = a.ids[lane];
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    wait_lgkm();
     __builtin_amdgcn_wave_barrier();
     if (lane < top_k) {
       const uint64_t* rt = a.routed_table + (size_t)s_sel[lane] * 3 * a.max_pages;
       s_tab[lane][0] = rt;
       s_tab[lane][1] = rt + a.max_pages;
     }
+    VIB3_TRACE_POINT(2);
   }
   __syncthreads();
+  VIB3_TRACE_POINT(3);
   if (!have) return;
   if (PAGED) {
     // lane k <- this wave's k-th item (lanes past the end keep a valid page-table row)
@@ -284,7 +320,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
       my_t1 = (uint64_t)(uintptr_t)s_tab[slot][1];
     }
   }
-  if (!early) start(buf[0], 0, false, it0);
+  if (!early_now) start(buf[0], 0, false, it0);
   // NB buffers in a ring: while item i is reduced, items i+1 .. i+NB-1 are loading
   for (int b = 1; b + 1 < kRowsBuffers; b++) start(buf[b], b, false, it0 + b * stride);
   load_x<NCH, SPLIT>(a.x, a.x_dt, cpr, cidx, xh, xl);
@@ -307,6 +343,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     const int q = item / M;
     store_out(a, (size_t)slot_of(q) * a.out_stride + (item - q * M), res);
   }
+  VIB3_TRACE_POINT(4);
 }
 
 template <int NCH, bool DUAL, bool SPLIT, bool PAGED>

@@ -31,10 +31,16 @@ struct RouterArgs {
   float* wts;          // [top_k]
   uint16_t* out_ids;   // optional copies for the caller
   float* out_wts;
+  // logits published in the gate/up kernel (fused routing): tagged slots, see select.h
+  uint64_t* slots;     // [E]
+  uint32_t gen;        // this launch's tag (never 0)
+  int* error;          // set to 1 if a wait gave up
 };
 
 int launch_router_logits(const RouterArgs& a, hipStream_t s, KTime t = {});
 int launch_router_select(const RouterArgs& a, hipStream_t s, KTime t = {});
+
+enum { kRouteGiven = 0, kRouteScores = 1, kRouteFused = 2 };
 
 // Experts whose selection fits the register path of select.h (8 keys per lane).
 constexpr int kMaxExpertsInKernel = 8 * 64;
@@ -59,8 +65,10 @@ struct RowsArgs {
   size_t out_stride;  // elements between slots in out
   int KS;             // waves that split one row's k range (set by the launcher)
   int RPT;            // rows per team
-  // When `route` is set, every workgroup selects the top-k of router.scores in its prologue
-  // (wave 0; block 0 also publishes router.ids / router.wts) instead of reading `ids`.
+  // route = kRouteGiven: slots take experts from `ids`. kRouteScores: every workgroup selects
+  // the top-k of router.scores in its prologue (wave 0; block 0 also publishes router.ids /
+  // router.wts). kRouteFused: workgroups first compute the router logits themselves (block b
+  // takes experts b, b + grid, ...), publish them as tagged slots, and then select as above.
   int route;
   RouterArgs router;
 };

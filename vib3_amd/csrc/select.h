@@ -119,26 +119,110 @@ __device__ __forceinline__ float wave_max_f(float v) {
 // best remaining candidate. A round is then branch-free: the wave maximum of the heads, a
 // ballot for the lanes that hold it (the lowest index wins a tie), and the winning lane pops
 // its head. The order of the picks is the order of a stable descending sort.
+// Fast path for top_k <= 8: no sequential rounds. Let t be the smallest of the eight
+// 8-lane-group maxima of the keys; those eight maxima are distinct experts with key >= t, so
+// the k-th best key is >= t and every expert of the top-k is a candidate (key >= t). The
+// candidates (typically a few dozen) are compacted into LDS, and each candidate's rank is the
+// number of candidates that beat it in the (key desc, index asc) order; ranks below k are the
+// picks, in order. Returns false (wave-uniformly) when more than 64 candidates pass the bound,
+// e.g. with many equal keys; the caller then runs the rounds.
 template <int R>
-__device__ inline void select_topk_regs(const RouterArgs& a, const float* scores, int* sel,
+__device__ inline bool select_fast(const RouterArgs& a, const float (&key)[R],
+                                   const float (&val)[R], const int (&idx)[R], int* sel,
+                                   float* selv) {
+  __shared__ __attribute__((aligned(16))) float ck[kWave];
+  __shared__ __attribute__((aligned(16))) int ci[kWave];
+  __shared__ float cv[kWave];
+  constexpr int kNone = 0x7fffffff;
+  const int lane = lane_id();
+  float m = -__builtin_huge_valf();
+#pragma unroll
+  for (int r = 0; r < R; r++)
+    if (idx[r] != kNone) m = fmaxf(m, key[r]);
+  m = fmaxf(m, dpp<0xB1>(m));   // quad_perm [1,0,3,2]
+  m = fmaxf(m, dpp<0x4E>(m));   // quad_perm [2,3,0,1]
+  m = fmaxf(m, dpp<0x141>(m));  // row_half_mirror: every lane holds its 8-lane group maximum
+  float t = __builtin_huge_valf();
+#pragma unroll
+  for (int g = 0; g < kWave; g += 8)
+    t = fminf(t, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), g)));
+  VIB3_TRACE_POINT(8);  // threshold
+  int n = 0;
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const bool c = idx[r] != kNone && key[r] >= t;
+    const uint64_t mask = __ballot(c);
+    const int pos = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+    if (c && pos < kWave) {
+      ck[pos] = key[r];
+      cv[pos] = val[r];
+      ci[pos] = idx[r];
+    }
+    n += __popcll(mask);
+  }
+  VIB3_TRACE_VALUE(7, n);
+  VIB3_TRACE_POINT(9);  // compacted
+  if (n > kWave) return false;
+  if (lane >= n && lane < ((n + 7) & ~7)) {  // pad to a multiple of 8: never beats anything
+    ck[lane] = -__builtin_huge_valf();
+    ci[lane] = kNone;
+  }
+  wait_lgkm();
+  __builtin_amdgcn_wave_barrier();
+  // every lane takes candidate `lane` and counts the candidates that beat it, reading the
+  // list from LDS eight at a time (broadcast reads, all issued before the compares)
+  const float mk = lane < n ? ck[lane] : -__builtin_huge_valf();
+  const int mi = lane < n ? ci[lane] : kNone;
+  const float mv = lane < n ? cv[lane] : 0.0f;
+  int rank = 0;
+  for (int j0 = 0; j0 < n; j0 += 8) {
+    const float4 ka = *(const float4*)(ck + j0), kb = *(const float4*)(ck + j0 + 4);
+    const int4 ia = *(const int4*)(ci + j0), ib = *(const int4*)(ci + j0 + 4);
+    const float kk[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+    const int ii[8] = {ia.x, ia.y, ia.z, ia.w, ib.x, ib.y, ib.z, ib.w};
+#pragma unroll
+    for (int u = 0; u < 8; u++) rank += (kk[u] > mk || (kk[u] == mk && ii[u] < mi)) ? 1 : 0;
+  }
+  if (lane < n && rank < a.top_k) {
+    sel[rank] = mi;
+    selv[rank] = mv;
+  }
+  VIB3_TRACE_POINT(10);  // ranked
+  wait_lgkm();
+  __builtin_amdgcn_wave_barrier();
+  return true;
+}
+
+// Top-k by the calling wave (all 64 lanes active) from scores already in registers: lane l
+// holds the scores of experts l, l+64, ... (sc[r] for expert l + 64r). Each lane first sorts
+// its keys by (key desc, index asc), so the lane heads hold every lane's best remaining
+// candidate. A round is then branch-free: the wave maximum of the heads, a ballot for the
+// lanes that hold it (the lowest index wins a tie), and the winning lane pops its head. The
+// order of the picks is the order of a stable descending sort.
+template <int R>
+__device__ inline void select_topk_vals(const RouterArgs& a, const float (&sc)[R], int* sel,
                                         float* selv, bool publish) {
   const int lane = lane_id();
   constexpr int kNone = 0x7fffffff;
-  float key[R], val[R], sc[R], bs[R];
+  float key[R], val[R], bs[R];
   int idx[R];
-  const float* bp = a.bias ? a.bias : scores;
 #pragma unroll
-  for (int r = 0; r < R; r++) {  // all loads first: one round trip, not R
-    const int e = min(lane + r * kWave, a.E - 1);
-    sc[r] = scores[e];
-    bs[r] = bp[e];
-  }
+  for (int r = 0; r < R; r++) bs[r] = a.bias ? a.bias[min(lane + r * kWave, a.E - 1)] : 0.0f;
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int e = lane + r * kWave;
-    selection_key(a, sc[r], a.bias ? bs[r] : 0.0f, key[r], val[r]);
+    selection_key(a, sc[r], bs[r], key[r], val[r]);
     if (e >= a.E) key[r] = -__builtin_huge_valf();
     idx[r] = e < a.E ? e : kNone;
+  }
+  VIB3_TRACE_POINT(5);  // scores and bias in registers
+  if (a.top_k <= 8 && select_fast<R>(a, key, val, idx, sel, selv)) {
+    VIB3_TRACE_POINT(6);  // picks done
+    router_weights_wave(a, sel, selv, publish);
+    wait_lgkm();
+    __builtin_amdgcn_wave_barrier();
+    return;
   }
   // insertion network: R(R-1)/2 compare-exchanges, all lanes in parallel
 #pragma unroll
@@ -178,11 +262,61 @@ __device__ inline void select_topk_regs(const RouterArgs& a, const float* scores
     key[R - 1] = pop ? -__builtin_huge_valf() : key[R - 1];
     idx[R - 1] = pop ? kNone : idx[R - 1];
   }
-  __builtin_amdgcn_s_waitcnt(0);
+  wait_lgkm();
   __builtin_amdgcn_wave_barrier();
+  VIB3_TRACE_POINT(6);  // picks done
   router_weights_wave(a, sel, selv, publish);
-  __builtin_amdgcn_s_waitcnt(0);
+  wait_lgkm();
   __builtin_amdgcn_wave_barrier();
+}
+
+// Same, loading the scores from memory first.
+template <int R>
+__device__ inline void select_topk_regs(const RouterArgs& a, const float* scores, int* sel,
+                                        float* selv, bool publish) {
+  float sc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) sc[r] = scores[min(lane_id() + r * kWave, a.E - 1)];
+  select_topk_vals<R>(a, sc, sel, selv, publish);
+}
+
+// Wait until every expert's logit of this launch is published in `slots` (one 64-bit word per
+// expert: generation tag << 32 | f32 bits, written with a device-scope atomic store by the
+// workgroup that computed it), then select. Tags make the wait independent of any ordering
+// between different addresses, so no device-wide fence is needed. The wait is bounded: after
+// kRouterSpinLimit polls the wave records an error and selects from what it has.
+constexpr int kRouterSpinLimit = 1 << 20;
+
+template <int R>
+__device__ inline void select_topk_published(const RouterArgs& a, int* sel, float* selv,
+                                             bool publish) {
+  const int lane = lane_id();
+  float sc[R];
+  for (int it = 0;; it++) {
+    bool ok = true;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int e = min(lane + r * kWave, a.E - 1);
+      const uint64_t v = __hip_atomic_load(a.slots + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok &= (uint32_t)(v >> 32) == a.gen;
+      sc[r] = __uint_as_float((uint32_t)v);
+    }
+    if (__all(ok)) break;
+    if (it >= kRouterSpinLimit) {
+      if (lane == 0) a.error[0] = 1;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  select_topk_vals<R>(a, sc, sel, selv, publish);
+}
+
+__device__ inline void select_topk_published_small(const RouterArgs& a, int* sel, float* selv,
+                                                   bool publish) {
+  if (a.E <= 2 * kWave) select_topk_published<2>(a, sel, selv, publish);
+  else if (a.E <= 4 * kWave) select_topk_published<4>(a, sel, selv, publish);
+  else if (a.E <= 6 * kWave) select_topk_published<6>(a, sel, selv, publish);
+  else select_topk_published<8>(a, sel, selv, publish);
 }
 
 // Register selection for up to 8 * 64 experts, with the register count matched to E.
@@ -217,10 +351,10 @@ __device__ inline void select_topk_lds(const RouterArgs& a, const float* scores,
     }
     if (lane == 0) sel[j] = win;
   }
-  __builtin_amdgcn_s_waitcnt(0);
+  wait_lgkm();
   __builtin_amdgcn_wave_barrier();
   router_weights_wave(a, sel, selv, publish);
-  __builtin_amdgcn_s_waitcnt(0);
+  wait_lgkm();
   __builtin_amdgcn_wave_barrier();
 }
 
