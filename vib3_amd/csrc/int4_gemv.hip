@@ -574,6 +574,7 @@ struct DownRowsBatch {
 
 template <int J, int NB>
 __global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
+  VIB3_TRACE_POINT(0);
   extern __shared__ uint4 lds[];
   constexpr int CP = 16 * J;  // chunks per slot in LDS, zero past the last chunk
   const int lane = lane_id();
@@ -671,33 +672,73 @@ __global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
   pos[0] = Pos{g0, 0};
 #pragma unroll
   for (int b = 1; b < NB; b++) pos[b] = advance(pos[b - 1]);
-  if (n > 0) {  // the first batches load while the activations are staged
-#pragma unroll
-    for (int b = 0; b + 1 < NB; b++) start(buf[b], pos[b], b >= n);
-  }
+  VIB3_TRACE_POINT(1);
+  // stage the activations: each thread takes up to three chunks per pass and issues all of
+  // their loads before converting any (one round trip per pass, not one per chunk)
   const char* hb = (const char*)a.h;
-  for (int i = (int)threadIdx.x; i < ns * CP; i += (int)blockDim.x) {
-    const int sl = i / CP, c = i - sl * CP;
-    XChunk hi, lo;
-    if (c < cpr) {
-      float xv[32];
-      load_chunk_act(hb + (size_t)sl * a.K * 2, VIB3_DT_F16, c, xv);
-      make_chunk(xv, hi, lo);
-    } else {
-      zero_chunk(hi);
+  const int nitem = ns * CP, bd = (int)blockDim.x;
+  auto load_raw = [&](int i0, uint4 (&raw)[3][4]) {
+#pragma unroll
+    for (int u = 0; u < 3; u++) {
+      const int i = min(i0 + u * bd, nitem - 1);
+      const int sl = i / CP, c = min(i - sl * CP, cpr - 1);
+      const uint4* src = (const uint4*)(hb + ((size_t)sl * a.K + (size_t)c * 32) * 2);
+#pragma unroll
+      for (int q = 0; q < 4; q++) raw[u][q] = src[q];
     }
-    uint4* xp = xq + (size_t)sl * 4 * CP + c;
-    auto pack = [](const h2 (&v)[4]) {
-      return make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
-                        __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
-    };
-    xp[0] = pack(hi.a);
-    xp[CP] = pack(hi.b);
-    xp[2 * CP] = pack(hi.c);
-    xp[3 * CP] = pack(hi.d);
-    xsum[sl * CP + c] = hi.xs8;
+  };
+  auto stage = [&](int i0, const uint4 (&raw)[3][4]) {
+#pragma unroll
+    for (int u = 0; u < 3; u++) {
+      const int i = i0 + u * bd;
+      if (i >= nitem) break;
+      const int sl = i / CP, c = i - sl * CP;
+      XChunk hi, lo;
+      if (c < cpr) {
+        float xv[32];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const uint32_t w[4] = {raw[u][q].x, raw[u][q].y, raw[u][q].z, raw[u][q].w};
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            xv[8 * q + 2 * j] = f16_to_f32((uint16_t)(w[j] & 0xffff));
+            xv[8 * q + 2 * j + 1] = f16_to_f32((uint16_t)(w[j] >> 16));
+          }
+        }
+        make_chunk(xv, hi, lo);
+      } else {
+        zero_chunk(hi);
+      }
+      uint4* xp = xq + (size_t)sl * 4 * CP + c;
+      auto pack = [](const h2 (&v)[4]) {
+        return make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                          __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
+      };
+      xp[0] = pack(hi.a);
+      xp[CP] = pack(hi.b);
+      xp[2 * CP] = pack(hi.c);
+      xp[3 * CP] = pack(hi.d);
+      xsum[sl * CP + c] = hi.xs8;
+    }
+  };
+  {
+    // first pass, every thread (indices clamped): the first weight batches go out behind the
+    // (cached) activations, so waiting for the activations does not wait for the weights
+    uint4 raw[3][4];
+    load_raw((int)threadIdx.x, raw);
+    if (n > 0) {
+#pragma unroll
+      for (int b = 0; b + 1 < NB; b++) start(buf[b], pos[b], b >= n);
+    }
+    stage((int)threadIdx.x, raw);
+  }
+  for (int i0 = (int)threadIdx.x + 3 * bd; i0 < nitem; i0 += 3 * bd) {
+    uint4 raw[3][4];
+    load_raw(i0, raw);
+    stage(i0, raw);
   }
   __syncthreads();
+  VIB3_TRACE_POINT(2);
   if (n == 0) return;
   for (int k = 0;; k += NB) {
 #pragma unroll
@@ -707,7 +748,10 @@ __global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
       pos[nb] = advance(pos[(nb + NB - 1) % NB]);
       start(buf[nb], pos[nb], k + b + NB - 1 >= n);
       finish(buf[b], pos[b]);
-      if (k + b + 1 >= n) return;
+      if (k + b + 1 >= n) {
+        VIB3_TRACE_POINT(3);
+        return;
+      }
     }
   }
 }
