@@ -67,7 +67,8 @@ __global__ void k_zero(uint4* p16, size_t n16, uint8_t* tail, size_t ntail) {
   if (i < ntail) tail[i] = 0;
 }
 
-// Workspace of the fused layer: [scores[E] | ids[k] | wts[k] | h[nslots][inter]].
+// Workspace of the fused layer: [scores[E] | ids[k] | wts[k] | router slots u64[E] | error |
+// h[nslots][inter]].
 struct LayerWs {
   size_t scores, ids, wts, slots, error, h, total;
 };

@@ -259,37 +259,41 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // a shared-expert row needs no routing: start its loads before the selection
   const bool early = have && PAGED && slot_of(it0 / M) >= top_k;
   // Fused routing: workgroup b computes router rows b, b + grid, ... and publishes each as a
-  // tagged slot. The first row's loads go out before the shared-expert row's, so the router,
-  // which every routed row waits for, is not queued behind the expert stream.
+  // tagged slot. The first row's loads go out before anything else, and a workgroup computing
+  // a router row starts its expert stream only after the selection, so the CU's memory
+  // pipeline serves the router rows, which every routed row waits for, first. (Cutting rows
+  // into halves to spread them evenly over the two workgroups of a CU measured slower.)
   const bool fused = PAGED && a.route == kRouteFused;
-  const bool split_row = fused && (int)blockIdx.x < a.router.E && router_row_splittable(a.router);
-  RouterRowRaw rrow;
-  if (split_row) router_row_issue(a.router, (int)blockIdx.x, rrow);
-  // a workgroup computing a router row starts its expert stream only after the selection: the
-  // CU's memory pipeline then serves the router rows, which every workgroup waits for, first
-  const bool early_now = early && !(fused && (int)blockIdx.x < a.router.E);
+  const int E = a.router.E, G = (int)gridDim.x;
+  auto publish = [&](int e, float v) {
+    if (threadIdx.x == 0) {
+      __hip_atomic_store(a.router.slots + e,
+                         ((uint64_t)a.router.gen << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      if (a.router.scores) a.router.scores[e] = v;
+    }
+  };
+  const bool split_row = fused && (int)blockIdx.x < E && router_seg_ok(a.router, 1, 4);
+  RouterSegRaw<4> rrow;
+  if (split_row) router_seg_issue<4>(a.router, (int)blockIdx.x, 0, 1, rrow);
+  const bool early_now = early && !(fused && (int)blockIdx.x < E);
   if (early_now) start(buf[0], 0, true, it0);
   if (fused) {
-    auto publish = [&](int e, float sc) {
-      if (threadIdx.x == 0) {
-        __hip_atomic_store(a.router.slots + e,
-                           ((uint64_t)a.router.gen << 32) | __float_as_uint(sc), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        if (a.router.scores) a.router.scores[e] = sc;
-      }
-    };
     int e = (int)blockIdx.x;
     if (split_row) {
-      publish(e, router_row_finish(a.router, rrow));
-      e += (int)gridDim.x;
+      publish(e, router_seg_finish<4>(a.router, 1, rrow));
+      e += G;
     }
-    for (; e < a.router.E; e += (int)gridDim.x) {
+    for (; e < E; e += G) {  // more rows than workgroups: one at a time
       publish(e, router_row_dot(a.router, e));
       __syncthreads();  // router_row_dot's reduction buffer is reused by the next row
     }
   }
   VIB3_TRACE_POINT(1);
   if (PAGED && top_k > 0 && wave == 0) {
+    // the selection is on every routed row's critical path: issue ahead of the streaming
+    // waves that share this SIMD
+    __builtin_amdgcn_s_setprio(3);
     if (a.route == kRouteFused) {
       select_topk_published_small(a.router, s_sel, s_wts, blockIdx.x == 0);
     } else if (a.route == kRouteScores) {
@@ -304,6 +308,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
       s_tab[lane][0] = rt;
       s_tab[lane][1] = rt + a.max_pages;
     }
+    __builtin_amdgcn_s_setprio(0);
     VIB3_TRACE_POINT(2);
   }
   __syncthreads();
@@ -848,8 +853,8 @@ static void launch_rows_p(RowsArgs& a, hipStream_t s, KTime t) {
     if (per_cu > 0 && per_cu * device_cus() < cap) cap = per_cu * device_cus();
     const int floor_blocks = (items + 4 * kWave - 1) / (4 * kWave);  // <= 64 items per wave
     if (cap < floor_blocks) cap = floor_blocks;
-    hipExtLaunchKernelGGL(k, dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0, s, t.start,
-                          t.stop, 0, a);
+    const int grid = want < cap ? want : cap;
+    hipExtLaunchKernelGGL(k, dim3((unsigned)grid), dim3(256), 0, s, t.start, t.stop, 0, a);
   } else {
     auto k = k_int4_rows_ksplit<N, D, S, P>;
     const int teams = 4 / a.KS;

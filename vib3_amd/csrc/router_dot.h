@@ -88,31 +88,37 @@ __device__ inline float router_row_dot(const RouterArgs& a, int e) {
 }
 
 // The same dot product split in two, so a caller can issue other loads in between: issue()
-// starts every load of the row (one batch: D <= 8192, 16-byte aligned rows), finish() waits for
-// them only and reduces. The load count does not depend on the dtypes (16-bit rows re-read
-// their chunk instead of a second one), so the wait counts stay exact. The result is bit for
-// bit that of router_row_dot.
-struct RouterRowRaw {
-  uint4 w[4][2], x[4][2];
+// starts every load of a row segment (segment `part` of `parts` equal pieces of row e, at most
+// 8 * U * 256 elements, 16-byte aligned), finish() waits for them only and reduces the
+// segment over the workgroup. The load count does not depend on the dtypes (16-bit rows
+// re-read their chunk instead of a second one), so the wait counts stay exact. For parts = 1,
+// U = 4 the result is bit for bit that of router_row_dot.
+template <int U>
+struct RouterSegRaw {
+  uint4 w[U][2], x[U][2];
 };
 
-__device__ inline bool router_row_splittable(const RouterArgs& a) {
-  return a.D % 8 == 0 && a.D <= 8 * 4 * 256 && (((uintptr_t)a.w) & 15) == 0 &&
+__device__ inline bool router_seg_ok(const RouterArgs& a, int parts, int U) {
+  return a.D % (8 * parts) == 0 && a.D / parts <= 8 * U * 256 && (((uintptr_t)a.w) & 15) == 0 &&
          (((uintptr_t)a.x) & 15) == 0;
 }
 
-__device__ inline void router_row_issue(const RouterArgs& a, int e, RouterRowRaw& r) {
-  const int tid = (int)threadIdx.x, n8 = a.D / 8;
+template <int U>
+__device__ inline void router_seg_issue(const RouterArgs& a, int e, int part, int parts,
+                                        RouterSegRaw<U>& r) {
+  const int tid = (int)threadIdx.x, n8 = a.D / (8 * parts);
   const int wsz = a.w_dt == VIB3_DT_F32 ? 32 : 16, xsz = a.x_dt == VIB3_DT_F32 ? 32 : 16;
-  const uint8_t* row = (const uint8_t*)a.w + (size_t)e * n8 * wsz;
+  const size_t g0 = (size_t)part * n8;  // first 8-element group of the segment
+  const uint8_t* row = (const uint8_t*)a.w + ((size_t)e * (a.D / 8) + g0) * wsz;
+  const uint8_t* xs = (const uint8_t*)a.x + g0 * xsz;
 #pragma unroll
-  for (int u = 0; u < 4; u++) {
+  for (int u = 0; u < U; u++) {
     const int i = u * 256 + tid;
     const int ic = i < n8 ? i : 0;
     r.w[u][0] = ld_stream(row + (size_t)ic * wsz);
     r.w[u][1] = ld_stream(row + (size_t)ic * wsz + (wsz - 16));
-    r.x[u][0] = *(const uint4*)((const uint8_t*)a.x + (size_t)ic * xsz);
-    r.x[u][1] = *(const uint4*)((const uint8_t*)a.x + (size_t)ic * xsz + (xsz - 16));
+    r.x[u][0] = *(const uint4*)(xs + (size_t)ic * xsz);
+    r.x[u][1] = *(const uint4*)(xs + (size_t)ic * xsz + (xsz - 16));
   }
 }
 
@@ -132,12 +138,13 @@ __device__ inline void raw8(const uint4 (&v)[2], int dt, float* o) {
   }
 }
 
-__device__ inline float router_row_finish(const RouterArgs& a, const RouterRowRaw& r) {
+template <int U>
+__device__ inline float router_seg_finish(const RouterArgs& a, int parts, const RouterSegRaw<U>& r) {
   __shared__ float red[4];
-  const int tid = (int)threadIdx.x, n8 = a.D / 8;
+  const int tid = (int)threadIdx.x, n8 = a.D / (8 * parts);
   float acc = 0.0f;
 #pragma unroll
-  for (int u = 0; u < 4; u++) {
+  for (int u = 0; u < U; u++) {
     if (u * 256 + tid < n8) {
       float w[8], x[8];
       raw8(r.w[u], a.w_dt, w);
@@ -150,7 +157,7 @@ __device__ inline float router_row_finish(const RouterArgs& a, const RouterRowRa
   if ((tid & 63) == 0) red[tid >> 6] = acc;
   __syncthreads();
   const float s = (red[0] + red[1]) + (red[2] + red[3]);
-  __syncthreads();  // red is reused by the next row
+  __syncthreads();  // red is reused by the next segment
   return s;
 }
 
