@@ -190,6 +190,12 @@ def bench_c4(args, cfg) -> int:
                          f"(8 experts each), median of {len(times)} reps, scaled x{T // len(sample)} "
                          f"to the 64-token batch"}
 
+    traffic = None  # HBM bytes per batch of the two GEMM launches, from the committed PMC summary
+    tpath = os.path.join(ROOT, "profiles", "traffic_c4.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            kern = json.load(f)["kernels"]
+        traffic = sum(kern[k]["hbm_bytes"] for k in kern)
     out = {
         "metric": "MoE batched decode us per 64-token batch (Kimi-K2.5 shape, MXFP4 experts)",
         "value": round(us, 2), "unit": "us/batch", "n_gpus": 1, "steps": args.steps,
@@ -202,7 +208,8 @@ def bench_c4(args, cfg) -> int:
                    "algorithmic_bytes_per_batch": round(avg_bytes)},
         "roofline": {"bound": "hbm", "kernel": "k_mx_gemm (gate/up + down grouped GEMM, whole batch)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": "profiles/traffic_c4.json" if traffic else None},
         "mfma": {"achieved_tflops": round(flops / (us * 1e-6) / 1e12, 2), "peak_tflops_bf16": 2500.0,
                  "frac": round(flops / (us * 1e-6) / 2.5e15, 5)},
         "tokens_per_s": round(T / (us * 1e-6)),
