@@ -200,10 +200,9 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   int my_row = 0;
   uint64_t my_t0 = 0, my_t1 = 0;
   RowBatch<NCH, DUAL, 1> buf[kRowsBuffers];
-  // start() is issued unconditionally: a batch past the last item reads the activation
-  // vector instead (all wave-uniform selects). A branch around the loads would leave the
-  // compiler's wait counting unsure how many loads are in flight, and it would then wait for
-  // all of them.
+  // start() is issued unconditionally, also for a batch past the last item (see below). A
+  // branch around the loads would leave the compiler's wait counting unsure how many loads are
+  // in flight, and it would then wait for all of them.
   auto start = [&](RowBatch<NCH, DUAL, 1>& buf, int k, bool direct, int item) {
     const bool past = item >= items;
     MatRef m0, m1;
@@ -217,7 +216,11 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
         t0 = shared_table_of(slot_of(q), 0);
         t1 = shared_table_of(slot_of(q), 1);
       } else {
-        k &= kWave - 1;  // k may run two past the last item; any lane holds a valid row
+        // A batch past this wave's last item re-reads the row just fetched (valid and still
+        // cached). Swapping in another base pointer instead would merge two address sources at
+        // the loop head and make the compiler wait for every load in flight there.
+        if (past) k -= 1;
+        k &= kWave - 1;
         row = __builtin_amdgcn_readlane(my_row, k);
         t0 = (const uint64_t*)(uintptr_t)(
             ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(my_t0 >> 32), k) << 32) |
@@ -234,8 +237,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
       m1 = a.flat1;
     }
     const int ra[1] = {row};
-    issue<PAGED, NCH, DUAL, 1>(buf, m0, m1, ra, cidx, gidx, pk, ng, cpr,
-                               past ? a.x : nullptr);
+    issue<PAGED, NCH, DUAL, 1>(buf, m0, m1, ra, cidx, gidx, pk, ng, cpr);
     // keep the scheduler from sinking these loads below the previous batch's arithmetic
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -464,9 +466,9 @@ __global__ __launch_bounds__(WIDE ? 1024 : 640) void k_down_combine(DownArgs a) 
     if (p.i0 >= ipb * RPB) { p.i0 = 0; p.bb += (int)gridDim.x; }
     return p;
   };
-  // start() runs unconditionally (see k_int4_rows): a batch past the end resolves row M - 1
-  // and then reads the activation buffer instead
-  auto start = [&](DownBatch<U>& b, Pos p, bool past) {
+  // start() runs unconditionally (see k_int4_rows); a batch past the end is given the position
+  // fetched just before it (rows clamp to M - 1, so every position is a valid one)
+  auto start = [&](DownBatch<U>& b, Pos p) {
     const int r0 = p.bb * a.RB, nr = min(a.RB, a.M - r0);
 #pragma unroll
     for (int u = 0; u < U; u++) {
@@ -481,10 +483,6 @@ __global__ __launch_bounds__(WIDE ? 1024 : 640) void k_down_combine(DownArgs a) 
         const uint16_t* sq;
         mat_row<true>(m, r, pk, ng, dq, sq);
         if (grp == q) { d = dq; sc = sq; }
-      }
-      if (past) {
-        d = (const uint8_t*)hbase;
-        sc = (const uint16_t*)hbase;
       }
 #pragma unroll
       for (int j = 0; j < kDownJ; j++) {
@@ -536,7 +534,7 @@ __global__ __launch_bounds__(WIDE ? 1024 : 640) void k_down_combine(DownArgs a) 
   DownBatch<U> A, B;
   Pos q0{(int)blockIdx.x, 0};
   Pos q1 = advance(q0);
-  start(A, q0, false);
+  start(A, q0);
   // activations: the 4 chunks of h this lane multiplies, loaded after the first weights
 #pragma unroll
   for (int j = 0; j < kDownJ; j++) {
@@ -551,11 +549,11 @@ __global__ __launch_bounds__(WIDE ? 1024 : 640) void k_down_combine(DownArgs a) 
     }
   }
   for (int k = 0;; k += 2) {
-    start(B, q1, k + 1 >= n);
+    start(B, k + 1 >= n ? q0 : q1);
     finish(A, q0);
     if (k + 1 >= n) break;
     q0 = advance(q1);
-    start(A, q0, k + 2 >= n);
+    start(A, k + 2 >= n ? q1 : q0);
     finish(B, q1);
     if (k + 2 >= n) break;
     q1 = advance(q0);
@@ -609,15 +607,17 @@ __global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
 
   const int G = (a.M + 3) / 4;  // row groups
   const int g0 = (int)blockIdx.x * 4 + wave;
-  const int gstride = (int)gridDim.x * 4;
-  const int ngr = g0 < G ? (G - 1 - g0) / gstride + 1 : 0;
-  const int n = ngr * ns;  // batches of this wave: (group, slot), slots innermost
+  // one row group per wave (the launcher sizes the grid so): its batches are the slots
+  const int n = g0 < G ? ns : 0;
   struct Pos { int g, s; };
   auto advance = [&](Pos p) {
-    if (++p.s == ns) { p.s = 0; p.g += gstride; }
+    p.s = min(p.s + 1, ns - 1);
     return p;
   };
-  auto start = [&](DownRowsBatch<J>& b, Pos p, bool past) {
+  // A batch past the end is given the position fetched just before it (valid, still cached):
+  // swapping in another base pointer would merge two address sources at the loop head and
+  // make the compiler wait for every load in flight there.
+  auto start = [&](DownRowsBatch<J>& b, Pos p) {
     const uint64_t tv =
         ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(my_t >> 32), p.s) << 32) |
         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)my_t, p.s);
@@ -632,10 +632,6 @@ __global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
       mat_row<true>(m, r, pk, ng, dq, sq);
       if (grp == q) { d = dq; sc = sq; }
     }
-    if (past) {  // a batch past the end reads the (cached) intermediate instead
-      d = (const uint8_t*)a.h;
-      sc = (const uint16_t*)a.h;
-    }
 #pragma unroll
     for (int j = 0; j < J; j++) {
       b.w[j] = ld_stream(d + (uint32_t)cld[j] * 16u);
@@ -644,7 +640,7 @@ __global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   };
   float o = 0.0f;
-  auto finish = [&](const DownRowsBatch<J>& b, Pos p) {
+  auto finish = [&](const DownRowsBatch<J>& b, Pos p, bool keep) {
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < J; j++) {
@@ -663,12 +659,8 @@ __global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
     if (a.round_f16) dsum = (float)(half_t)dsum;
     const float w = p.s < top_k ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), p.s))
                                 : 1.0f;
-    o = add_mul_rn(o, w, dsum);  // weighted_accumulate_f32 in slot order (engine.rs:5262-5302)
-    if (p.s == ns - 1) {
-      const int r = 4 * p.g + grp;
-      if (sub == 0 && r < a.M) a.out[r] = o;
-      o = 0.0f;
-    }
+    const float next = add_mul_rn(o, w, dsum);  // weighted_accumulate_f32 in slot order
+    o = keep ? next : o;                         // (engine.rs:5262-5302)
   };
 
   // NB load buffers in a ring: while batch i is reduced, batches i+1 .. i+NB-1 are loading
@@ -693,6 +685,14 @@ __global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
     }
   };
   auto stage = [&](int i0, const uint4 (&raw)[3][4]) {
+    // Every lane takes delivery of its raw words here, outside the lane-masked region below:
+    // a wait inside a region that the wave can skip would leave the compiler unsure whether
+    // these loads are done, and it would then wait for every load in flight in the main loop.
+#pragma unroll
+    for (int u = 0; u < 3; u++)
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        asm volatile("" ::"v"(raw[u][q].x), "v"(raw[u][q].y), "v"(raw[u][q].z), "v"(raw[u][q].w));
 #pragma unroll
     for (int u = 0; u < 3; u++) {
       const int i = i0 + u * bd;
@@ -731,10 +731,10 @@ __global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
     // (cached) activations, so waiting for the activations does not wait for the weights
     uint4 raw[3][4];
     load_raw((int)threadIdx.x, raw);
-    if (n > 0) {
+    // (also for a wave with no batches: every position is valid, and a branch here would make
+    // the waits below count for both cases, i.e. wait for the weights too)
 #pragma unroll
-      for (int b = 0; b + 1 < NB; b++) start(buf[b], pos[b], b >= n);
-    }
+    for (int b = 0; b + 1 < NB; b++) start(buf[b], pos[b]);  // rows clamp to M - 1
     stage((int)threadIdx.x, raw);
   }
   for (int i0 = (int)threadIdx.x + 3 * bd; i0 < nitem; i0 += 3 * bd) {
@@ -745,20 +745,26 @@ __global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
   __syncthreads();
   VIB3_TRACE_POINT(2);
   if (n == 0) return;
-  for (int k = 0;; k += NB) {
+  // The loop always runs whole rounds of NB batches, and a batch past the end is reduced like
+  // the others and then dropped (a select, not a branch): an exit between two batches would
+  // give the loop head a path on which a buffer is still loading, and the compiler would then
+  // wait there for every load in flight.
+  for (int k = 0; k < n; k += NB) {
 #pragma unroll
     for (int b = 0; b < NB; b++) {
       // refill the buffer consumed last with batch k + b + NB - 1
       const int nb = (b + NB - 1) % NB;
-      pos[nb] = advance(pos[(nb + NB - 1) % NB]);
-      start(buf[nb], pos[nb], k + b + NB - 1 >= n);
-      finish(buf[b], pos[b]);
-      if (k + b + 1 >= n) {
-        VIB3_TRACE_POINT(3);
-        return;
-      }
+      const Pos prev = pos[(nb + NB - 1) % NB];
+      pos[nb] = advance(prev);
+      start(buf[nb], k + b + NB - 1 >= n ? prev : pos[nb]);
+      finish(buf[b], pos[b], k + b < n);
     }
   }
+  // stored after the loop: a store inside it would share the load counter with the weight
+  // loads, and the compiler then waits for all of them at the loop head
+  const int r = 4 * g0 + grp;
+  if (sub == 0 && r < a.M) a.out[r] = o;
+  VIB3_TRACE_POINT(3);
 }
 
 // ------------------------------------------------------------------------- k_int4_generic
