@@ -156,10 +156,6 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, size_t o, float v) 
 // stride over them (grid sized to the resident capacity), so all CUs stay busy to the end.
 // KS > 1: the KS waves of a team split one row's k range and combine through LDS.
 
-#ifndef VIB3_ROWS_BUFFERS
-#define VIB3_ROWS_BUFFERS 2  // load buffers per wave (build-time tuning knob)
-#endif
-constexpr int kRowsBuffers = VIB3_ROWS_BUFFERS;
 
 template <int NCH, bool DUAL, bool SPLIT, bool PAGED>
 __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
@@ -170,9 +166,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   XChunk xh[NCH], xl[NCH];
   int cidx[NCH], gidx[NCH];
 
-  // Items are (slot, row), shared-expert slots first; waves stride over them. Three load
-  // buffers rotate so the next two items' 16-byte loads are in flight while the current one
-  // is reduced (no register copies of in-flight loads, which would force a wait).
+  // Items are (slot, row), shared-expert slots first; waves stride over them.
   __shared__ int s_sel[64];
   __shared__ float s_wts[64];
   // per slot: page-table row of each matrix (resolved once; a 16-bit id load in the loop
@@ -199,7 +193,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // prefetched weight loads.
   int my_row = 0;
   uint64_t my_t0 = 0, my_t1 = 0;
-  RowBatch<NCH, DUAL, 1> buf[kRowsBuffers];
+  RowBatch<NCH, DUAL, 1> buf[2];
   // start() is issued unconditionally, also for a batch past the last item (see below). A
   // branch around the loads would leave the compiler's wait counting unsure how many loads are
   // in flight, and it would then wait for all of them.
@@ -291,6 +285,10 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
       __syncthreads();  // router_row_dot's reduction buffer is reused by the next row
     }
   }
+  // the activations, while the routing is pending; the selecting wave of a launch without
+  // fused routing selects first (its loads would queue behind its early batch)
+  const bool sel_first = wave == 0 && !fused;
+  if (!sel_first) load_x<NCH, SPLIT>(a.x, a.x_dt, cpr, cidx, xh, xl);
   VIB3_TRACE_POINT(1);
   if (PAGED && top_k > 0 && wave == 0) {
     // the selection is on every routed row's critical path: issue ahead of the streaming
@@ -313,6 +311,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     __builtin_amdgcn_s_setprio(0);
     VIB3_TRACE_POINT(2);
   }
+  if (sel_first) load_x<NCH, SPLIT>(a.x, a.x_dt, cpr, cidx, xh, xl);
   __syncthreads();
   VIB3_TRACE_POINT(3);
   if (!have) return;
@@ -328,15 +327,19 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     }
   }
   if (!early_now) start(buf[0], 0, false, it0);
-  // NB buffers in a ring: while item i is reduced, items i+1 .. i+NB-1 are loading
-  for (int b = 1; b + 1 < kRowsBuffers; b++) start(buf[b], b, false, it0 + b * stride);
-  load_x<NCH, SPLIT>(a.x, a.x_dt, cpr, cidx, xh, xl);
-  for (int k = 0;; k += kRowsBuffers) {
+  // Two buffers: item k + 1's loads go out, then item k is reduced. Each step first takes
+  // delivery of everything in flight, so a wave has one item's loads (8 KB for a gate/up row
+  // pair of k = 7168) outstanding at a time: streaming measured fastest with about that much
+  // in flight per wave (two items per wave in flight, or a third buffer, measured slower).
+  // The explicit wait also makes the step independent of how the compiler counts loads at
+  // the loop head.
+  for (int k = 0;; k += 2) {
     bool done = false;
 #pragma unroll
-    for (int b = 0; b < kRowsBuffers; b++) {
-      const int ahead = k + b + kRowsBuffers - 1;
-      start(buf[(b + kRowsBuffers - 1) % kRowsBuffers], ahead, false, it0 + ahead * stride);
+    for (int b = 0; b < 2; b++) {
+      const int ahead = k + b + 1;
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      start(buf[(b + 1) % 2], ahead, false, it0 + ahead * stride);
       finish(buf[b]);
       if (it0 + (k + b + 1) * stride >= items) {
         done = true;
@@ -576,7 +579,7 @@ struct DownRowsBatch {
 };
 
 template <int J, int NB>
-__global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
+__global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
   VIB3_TRACE_POINT(0);
   extern __shared__ uint4 lds[];
   constexpr int CP = 16 * J;  // chunks per slot in LDS, zero past the last chunk
@@ -606,7 +609,7 @@ __global__ __launch_bounds__(256) void k_down_rows(DownArgs a) {
   }
 
   const int G = (a.M + 3) / 4;  // row groups
-  const int g0 = (int)blockIdx.x * 4 + wave;
+  const int g0 = (int)blockIdx.x * (int)(blockDim.x >> 6) + wave;
   // one row group per wave (the launcher sizes the grid so): its batches are the slots
   const int n = g0 < G ? ns : 0;
   struct Pos { int g, s; };
@@ -929,9 +932,14 @@ static size_t down_rows_lds(int nslots, int J) { return (size_t)nslots * 16 * J 
 
 template <int J>
 static void launch_down_rows_t(DownArgs& a, hipStream_t s, KTime t) {
+  // One row group per wave, and as many waves per workgroup as make one workgroup per CU
+  // (2..8): every CU streams the same share of the weights, and stages the activations once.
+  // (Four-wave workgroups left some CUs two workgroups and others one.)
   const int groups = (a.M + 3) / 4;
-  const int blocks = (groups + 3) / 4;
-  hipExtLaunchKernelGGL((k_down_rows<J, kDownRowsBuffers>), dim3((unsigned)blocks), dim3(256),
+  int wpb = env_int("VIB3_DOWN_WAVES", (groups + device_cus() - 1) / device_cus());
+  wpb = wpb < 2 ? 2 : wpb > 8 ? 8 : wpb;
+  const int blocks = (groups + wpb - 1) / wpb;
+  hipExtLaunchKernelGGL((k_down_rows<J, kDownRowsBuffers>), dim3((unsigned)blocks), dim3(64 * wpb),
                         (unsigned)down_rows_lds(a.nslots, J), s, t.start, t.stop, 0, a);
 }
 

@@ -182,7 +182,8 @@ __device__ inline bool select_fast(const RouterArgs& a, const float (&key)[R],
     const float kk[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
     const int ii[8] = {ia.x, ia.y, ia.z, ia.w, ib.x, ib.y, ib.z, ib.w};
 #pragma unroll
-    for (int u = 0; u < 8; u++) rank += (kk[u] > mk || (kk[u] == mk && ii[u] < mi)) ? 1 : 0;
+    for (int u = 0; u < 8; u++)  // bitwise, not short-circuit: no branches in the count
+      rank += (int)(kk[u] > mk) | ((int)(kk[u] == mk) & (int)(ii[u] < mi));
   }
   if (lane < n && rank < a.top_k) {
     sel[rank] = mi;
@@ -200,15 +201,21 @@ __device__ inline bool select_fast(const RouterArgs& a, const float (&key)[R],
 // candidate. A round is then branch-free: the wave maximum of the heads, a ballot for the
 // lanes that hold it (the lowest index wins a tie), and the winning lane pops its head. The
 // order of the picks is the order of a stable descending sort.
+// Bias of experts lane, lane + 64, ... (0 without a bias).
 template <int R>
-__device__ inline void select_topk_vals(const RouterArgs& a, const float (&sc)[R], int* sel,
-                                        float* selv, bool publish) {
+__device__ __forceinline__ void load_bias(const RouterArgs& a, float (&bs)[R]) {
+#pragma unroll
+  for (int r = 0; r < R; r++) bs[r] = a.bias ? a.bias[min(lane_id() + r * kWave, a.E - 1)] : 0.0f;
+}
+
+template <int R>
+__device__ inline void select_topk_vals(const RouterArgs& a, const float (&sc)[R],
+                                        const float (&bs)[R], int* sel, float* selv,
+                                        bool publish) {
   const int lane = lane_id();
   constexpr int kNone = 0x7fffffff;
-  float key[R], val[R], bs[R];
+  float key[R], val[R];
   int idx[R];
-#pragma unroll
-  for (int r = 0; r < R; r++) bs[r] = a.bias ? a.bias[min(lane + r * kWave, a.E - 1)] : 0.0f;
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int e = lane + r * kWave;
@@ -274,10 +281,11 @@ __device__ inline void select_topk_vals(const RouterArgs& a, const float (&sc)[R
 template <int R>
 __device__ inline void select_topk_regs(const RouterArgs& a, const float* scores, int* sel,
                                         float* selv, bool publish) {
-  float sc[R];
+  float sc[R], bs[R];
 #pragma unroll
   for (int r = 0; r < R; r++) sc[r] = scores[min(lane_id() + r * kWave, a.E - 1)];
-  select_topk_vals<R>(a, sc, sel, selv, publish);
+  load_bias<R>(a, bs);
+  select_topk_vals<R>(a, sc, bs, sel, selv, publish);
 }
 
 // Wait until every expert's logit of this launch is published in `slots` (one 64-bit word per
@@ -291,7 +299,8 @@ template <int R>
 __device__ inline void select_topk_published(const RouterArgs& a, int* sel, float* selv,
                                              bool publish) {
   const int lane = lane_id();
-  float sc[R];
+  float sc[R], bs[R];
+  load_bias<R>(a, bs);  // before the wait, off the critical path
   for (int it = 0;; it++) {
     bool ok = true;
 #pragma unroll
@@ -308,7 +317,7 @@ __device__ inline void select_topk_published(const RouterArgs& a, int* sel, floa
     }
     __builtin_amdgcn_s_sleep(1);
   }
-  select_topk_vals<R>(a, sc, sel, selv, publish);
+  select_topk_vals<R>(a, sc, bs, sel, selv, publish);
 }
 
 __device__ inline void select_topk_published_small(const RouterArgs& a, int* sel, float* selv,
