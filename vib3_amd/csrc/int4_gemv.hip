@@ -34,6 +34,17 @@ struct RowBatch {
   uint16_t q0[U][NCH], q1[U][NCH];
 };
 
+// Data and scale rows of row r of a paged matrix whose page (r's) starts at `base`.
+__device__ __forceinline__ void page_row(const uint8_t* base, int r, int rpp, int rows,
+                                         uint64_t magic, int pk, int ng, const uint8_t*& d,
+                                         const uint16_t*& s) {
+  const int p = (int)(((uint64_t)(uint32_t)r * magic) >> 32);
+  const int rr = r - p * rpp;
+  const int rows_here = min(rpp, rows - p * rpp);
+  d = base + (size_t)rr * pk;
+  s = (const uint16_t*)(base + (size_t)rows_here * pk) + (size_t)rr * ng;
+}
+
 template <bool PAGED, int NCH, bool DUAL, int U>
 __device__ __forceinline__ void issue(RowBatch<NCH, DUAL, U>& b, const MatRef& m0, const MatRef& m1,
                                       const int (&ra)[U], const int (&cidx)[NCH],
@@ -591,8 +602,14 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
   uint4* xq = lds;                                      // [ns][4][CP] pair words
   float* xsum = (float*)(lds + (size_t)ns * 4 * CP);    // [ns][CP] offset term
 
-  // lane s < nslots holds slot s's page-table row (down segment) and router weight
-  uint64_t my_t = 0;
+  const int G = (a.M + 3) / 4;  // row groups
+  const int g0 = (int)blockIdx.x * (int)(blockDim.x >> 6) + wave;
+  // lane s < nslots holds slot s's page-table row (down segment), router weight and, when
+  // pages hold whole row groups, the address of the page holding this wave's rows: the loop
+  // then reads no page table (a scalar table read per batch would delay every batch's loads
+  // by its latency)
+  const bool group_pages = a.rpp % 4 == 0;
+  uint64_t my_t = 0, my_base = 0;
   float my_w = 1.0f;
   if (lane < ns) {
     const uint64_t* t =
@@ -600,6 +617,11 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
                      : a.shared_table + ((size_t)(lane - top_k) * 3 + 2) * a.max_pages;
     my_t = (uint64_t)(uintptr_t)t;
     if (lane < top_k) my_w = a.wts[lane];
+    if (group_pages) {
+      typedef __attribute__((address_space(1))) const uint64_t gtab;
+      const int r0 = min(4 * g0, a.M - 1);
+      my_base = *(gtab*)(t + (int)(((uint64_t)(uint32_t)r0 * a.magic) >> 32));
+    }
   }
   int cld[J], gidx[J];
 #pragma unroll
@@ -608,8 +630,6 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
     gidx[j] = (cld[j] * 32) / a.g;
   }
 
-  const int G = (a.M + 3) / 4;  // row groups
-  const int g0 = (int)blockIdx.x * (int)(blockDim.x >> 6) + wave;
   // one row group per wave (the launcher sizes the grid so): its batches are the slots
   const int n = g0 < G ? ns : 0;
   struct Pos { int g, s; };
@@ -620,20 +640,27 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
   // A batch past the end is given the position fetched just before it (valid, still cached):
   // swapping in another base pointer would merge two address sources at the loop head and
   // make the compiler wait for every load in flight there.
+  auto rl64 = [&](uint64_t v, int l) {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
+           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  };
   auto start = [&](DownRowsBatch<J>& b, Pos p) {
-    const uint64_t tv =
-        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(my_t >> 32), p.s) << 32) |
-        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)my_t, p.s);
-    const MatRef m{(const uint64_t*)(uintptr_t)tv, nullptr, nullptr, a.rpp, a.M, a.magic};
     const uint8_t* d = nullptr;
     const uint16_t* sc = nullptr;
+    if (group_pages) {  // every lane its own row of the group's page
+      page_row((const uint8_t*)(uintptr_t)rl64(my_base, p.s), min(4 * p.g + grp, a.M - 1),
+               a.rpp, a.M, a.magic, pk, ng, d, sc);
+    } else {
+      const MatRef m{(const uint64_t*)(uintptr_t)rl64(my_t, p.s), nullptr, nullptr, a.rpp, a.M,
+                     a.magic};
 #pragma unroll
-    for (int q = 0; q < 4; q++) {  // the four rows are wave-uniform: scalar table reads
-      const int r = min(4 * p.g + q, a.M - 1);
-      const uint8_t* dq;
-      const uint16_t* sq;
-      mat_row<true>(m, r, pk, ng, dq, sq);
-      if (grp == q) { d = dq; sc = sq; }
+      for (int q = 0; q < 4; q++) {  // the four rows are wave-uniform: scalar table reads
+        const int r = min(4 * p.g + q, a.M - 1);
+        const uint8_t* dq;
+        const uint16_t* sq;
+        mat_row<true>(m, r, pk, ng, dq, sq);
+        if (grp == q) { d = dq; sc = sq; }
+      }
     }
 #pragma unroll
     for (int j = 0; j < J; j++) {
