@@ -205,9 +205,9 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   int my_row = 0;
   uint64_t my_t0 = 0, my_t1 = 0;
   RowBatch<NCH, DUAL, 1> buf[2];
-  // start() is issued unconditionally, also for a batch past the last item (see below). A
-  // branch around the loads would leave the compiler's wait counting unsure how many loads are
-  // in flight, and it would then wait for all of them.
+  // start() is issued unconditionally, also for a batch past the last item (its loads then
+  // read the activation vector). A branch around the loads would leave the compiler unsure
+  // how many loads are in flight.
   auto start = [&](RowBatch<NCH, DUAL, 1>& buf, int k, bool direct, int item) {
     const bool past = item >= items;
     MatRef m0, m1;
@@ -221,10 +221,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
         t0 = shared_table_of(slot_of(q), 0);
         t1 = shared_table_of(slot_of(q), 1);
       } else {
-        // A batch past this wave's last item re-reads the row just fetched (valid and still
-        // cached). Swapping in another base pointer instead would merge two address sources at
-        // the loop head and make the compiler wait for every load in flight there.
-        if (past) k -= 1;
+        if (past) k -= 1;  // any valid lane; the loads go to the activation vector instead
         k &= kWave - 1;
         row = __builtin_amdgcn_readlane(my_row, k);
         t0 = (const uint64_t*)(uintptr_t)(
@@ -242,7 +239,8 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
       m1 = a.flat1;
     }
     const int ra[1] = {row};
-    issue<PAGED, NCH, DUAL, 1>(buf, m0, m1, ra, cidx, gidx, pk, ng, cpr);
+    // a batch past the end reads the (cached) activation vector: no HBM traffic
+    issue<PAGED, NCH, DUAL, 1>(buf, m0, m1, ra, cidx, gidx, pk, ng, cpr, past ? a.x : nullptr);
     // keep the scheduler from sinking these loads below the previous batch's arithmetic
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -637,14 +635,13 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
     p.s = min(p.s + 1, ns - 1);
     return p;
   };
-  // A batch past the end is given the position fetched just before it (valid, still cached):
-  // swapping in another base pointer would merge two address sources at the loop head and
-  // make the compiler wait for every load in flight there.
+  // start() runs unconditionally; a batch past the end reads the intermediate (cached in
+  // L2) instead of weights.
   auto rl64 = [&](uint64_t v, int l) {
     return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
   };
-  auto start = [&](DownRowsBatch<J>& b, Pos p) {
+  auto start = [&](DownRowsBatch<J>& b, Pos p, bool past) {
     const uint8_t* d = nullptr;
     const uint16_t* sc = nullptr;
     if (group_pages) {  // every lane its own row of the group's page
@@ -661,6 +658,10 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
         mat_row<true>(m, r, pk, ng, dq, sq);
         if (grp == q) { d = dq; sc = sq; }
       }
+    }
+    if (past) {
+      d = (const uint8_t*)a.h;
+      sc = (const uint16_t*)a.h;
     }
 #pragma unroll
     for (int j = 0; j < J; j++) {
@@ -764,7 +765,7 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
     // (also for a wave with no batches: every position is valid, and a branch here would make
     // the waits below count for both cases, i.e. wait for the weights too)
 #pragma unroll
-    for (int b = 0; b + 1 < NB; b++) start(buf[b], pos[b]);  // rows clamp to M - 1
+    for (int b = 0; b + 1 < NB; b++) start(buf[b], pos[b], false);  // rows clamp to M - 1
     stage((int)threadIdx.x, raw);
   }
   for (int i0 = (int)threadIdx.x + 3 * bd; i0 < nitem; i0 += 3 * bd) {
@@ -784,9 +785,11 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
     for (int b = 0; b < NB; b++) {
       // refill the buffer consumed last with batch k + b + NB - 1
       const int nb = (b + NB - 1) % NB;
-      const Pos prev = pos[(nb + NB - 1) % NB];
-      pos[nb] = advance(prev);
-      start(buf[nb], k + b + NB - 1 >= n ? prev : pos[nb]);
+      pos[nb] = advance(pos[(nb + NB - 1) % NB]);
+      // (the explicit wait: see k_int4_rows; here it keeps the compiler's count exact with
+      // the past-the-end batches, which read the cached intermediate instead of weights)
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      start(buf[nb], pos[nb], k + b + NB - 1 >= n);
       finish(buf[b], pos[b], k + b < n);
     }
   }
