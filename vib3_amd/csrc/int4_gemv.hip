@@ -576,10 +576,11 @@ __global__ __launch_bounds__(WIDE ? 1024 : 640) void k_down_combine(DownArgs a) 
 //
 // Down projection + weighted combine with the activations of every slot staged once per
 // workgroup in LDS, already in chunk_dot's pair layout (so a batch costs no conversion work).
-// A wave owns a group of 4 output rows (16 lanes per row, J chunks per lane) and walks the
-// slots in router order, so the combine o = o + w_s * d_s happens in registers in the
-// reference's order: no cross-wave reduction, no barrier in the loop. f16 intermediates and
-// k <= 64 * 32 only; other shapes use k_down_combine.
+// A wave owns a group of R output rows (64 / R lanes per row, J chunks per lane per pass) and
+// walks the slots in router order, each slot in ceil(chunks / (64 / R * J)) passes over k, so
+// the combine o = o + w_s * d_s happens in registers in the reference's order: no cross-wave
+// reduction, no barrier in the loop. f16 intermediates whose staged form fits 64 KB of LDS;
+// other shapes use k_down_combine.
 
 template <int J>
 struct DownRowsBatch {
@@ -587,26 +588,42 @@ struct DownRowsBatch {
   uint16_t q[J];
 };
 
-template <int J, int NB>
+// Sum over each run of L lanes (L = 16, 32 or 64); every lane gets its run's total.
+template <int L>
+__device__ __forceinline__ float lanes_sum(float v) {
+  v = row16_sum(v);
+  if (L >= 32) v += __shfl_xor(v, 16);
+  if (L >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+template <int R, int J, int NB, bool ONE>  // ONE: the whole row in one pass (cpr <= CPP)
 __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
   VIB3_TRACE_POINT(0);
   extern __shared__ uint4 lds[];
-  constexpr int CP = 16 * J;  // chunks per slot in LDS, zero past the last chunk
+  constexpr int L = kWave / R;  // lanes per row
+  constexpr int CPP = L * J;    // chunks per pass
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int grp = lane >> 4, sub = lane & 15;
+  const int grp = lane / L, sub = lane % L;
   const int cpr = a.K / 32, pk = a.K / 2, ng = (a.K + a.g - 1) / a.g;
+  const int P = ONE ? 1 : (cpr + CPP - 1) / CPP;  // passes per slot
   const int ns = a.nslots, top_k = a.top_k;
-  uint4* xq = lds;                                      // [ns][4][CP] pair words
-  float* xsum = (float*)(lds + (size_t)ns * 4 * CP);    // [ns][CP] offset term
+  const int CT = ONE ? CPP : cpr;  // chunks per slot in LDS (one pass: zero past cpr)
+  uint4* xq = lds;                                       // [ns][4][CT] pair words
+  float* xsum = (float*)(lds + (size_t)ns * 4 * CT);     // [ns][CT] offset term
 
-  const int G = (a.M + 3) / 4;  // row groups
+  const int G = (a.M + R - 1) / R;  // row groups
   const int g0 = (int)blockIdx.x * (int)(blockDim.x >> 6) + wave;
+  // scale index of chunk c: (32 c) / g, a shift for the usual power-of-two group sizes
+  const bool g_pow2 = (a.g & (a.g - 1)) == 0;
+  const int g_shift = __builtin_ctz((unsigned)a.g);
+  auto scale_of = [&](int c) { return g_pow2 ? (c * 32) >> g_shift : (c * 32) / a.g; };
   // lane s < nslots holds slot s's page-table row (down segment), router weight and, when
   // pages hold whole row groups, the address of the page holding this wave's rows: the loop
   // then reads no page table (a scalar table read per batch would delay every batch's loads
   // by its latency)
-  const bool group_pages = a.rpp % 4 == 0;
+  const bool group_pages = a.rpp % R == 0;
   uint64_t my_t = 0, my_base = 0;
   float my_w = 1.0f;
   if (lane < ns) {
@@ -617,46 +634,43 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
     if (lane < top_k) my_w = a.wts[lane];
     if (group_pages) {
       typedef __attribute__((address_space(1))) const uint64_t gtab;
-      const int r0 = min(4 * g0, a.M - 1);
+      const int r0 = min(R * g0, a.M - 1);
       my_base = *(gtab*)(t + (int)(((uint64_t)(uint32_t)r0 * a.magic) >> 32));
     }
   }
-  int cld[J], gidx[J];
-#pragma unroll
-  for (int j = 0; j < J; j++) {
-    cld[j] = min(sub + 16 * j, cpr - 1);
-    gidx[j] = (cld[j] * 32) / a.g;
-  }
 
-  // one row group per wave (the launcher sizes the grid so): its batches are the slots
-  const int n = g0 < G ? ns : 0;
-  struct Pos { int g, s; };
-  auto advance = [&](Pos p) {
-    p.s = min(p.s + 1, ns - 1);
-    return p;
+  // one row group per wave (the launcher sizes the grid so); its batches are (slot, pass),
+  // passes innermost
+  const int n = g0 < G ? ns * P : 0;
+  struct Pos { int s, p; };
+  auto advance = [&](Pos q) {
+    if (++q.p == P) {
+      q.p = 0;
+      q.s = min(q.s + 1, ns - 1);
+    }
+    return q;
   };
-  // start() runs unconditionally; a batch past the end reads the intermediate (cached in
-  // L2) instead of weights.
   auto rl64 = [&](uint64_t v, int l) {
     return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
   };
-  auto start = [&](DownRowsBatch<J>& b, Pos p, bool past) {
+  // start() runs unconditionally; a batch past the end reads the intermediate (cached in
+  // L2) instead of weights. Lanes past the last chunk re-read it (their x is taken as zero).
+  auto start = [&](DownRowsBatch<J>& b, Pos q, bool past) {
     const uint8_t* d = nullptr;
     const uint16_t* sc = nullptr;
     if (group_pages) {  // every lane its own row of the group's page
-      page_row((const uint8_t*)(uintptr_t)rl64(my_base, p.s), min(4 * p.g + grp, a.M - 1),
+      page_row((const uint8_t*)(uintptr_t)rl64(my_base, q.s), min(R * g0 + grp, a.M - 1),
                a.rpp, a.M, a.magic, pk, ng, d, sc);
     } else {
-      const MatRef m{(const uint64_t*)(uintptr_t)rl64(my_t, p.s), nullptr, nullptr, a.rpp, a.M,
+      const MatRef m{(const uint64_t*)(uintptr_t)rl64(my_t, q.s), nullptr, nullptr, a.rpp, a.M,
                      a.magic};
 #pragma unroll
-      for (int q = 0; q < 4; q++) {  // the four rows are wave-uniform: scalar table reads
-        const int r = min(4 * p.g + q, a.M - 1);
+      for (int r = 0; r < R; r++) {  // the rows are wave-uniform: scalar table reads
         const uint8_t* dq;
         const uint16_t* sq;
-        mat_row<true>(m, r, pk, ng, dq, sq);
-        if (grp == q) { d = dq; sc = sq; }
+        mat_row<true>(m, min(R * g0 + r, a.M - 1), pk, ng, dq, sq);
+        if (grp == r) { d = dq; sc = sq; }
       }
     }
     if (past) {
@@ -665,51 +679,57 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < J; j++) {
-      b.w[j] = ld_stream(d + (uint32_t)cld[j] * 16u);
-      b.q[j] = ld_u16(sc + gidx[j]);
+      const int c = min(q.p * CPP + sub + L * j, cpr - 1);
+      b.w[j] = ld_stream(d + (uint32_t)c * 16u);
+      b.q[j] = ld_u16(sc + scale_of(c));
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  float o = 0.0f;
-  auto finish = [&](const DownRowsBatch<J>& b, Pos p, bool keep) {
-    float acc = 0.0f;
+  float o = 0.0f, acc = 0.0f;
+  auto finish = [&](const DownRowsBatch<J>& b, Pos q, bool keep) {
 #pragma unroll
     for (int j = 0; j < J; j++) {
-      const int c = sub + 16 * j;
-      const uint4* xp = xq + (size_t)p.s * 4 * CP + c;
+      const int c0 = q.p * CPP + sub + L * j;
+      const int c = ONE ? c0 : min(c0, cpr - 1);
+      const uint4* xp = xq + (size_t)q.s * 4 * CT + c;
       XChunk x;
-      const uint4 va = xp[0], vb = xp[CP], vc = xp[2 * CP], vd = xp[3 * CP];
+      const uint4 va = xp[0], vb = xp[CT], vc = xp[2 * CT], vd = xp[3 * CT];
       x.a[0] = as_h2(va.x); x.a[1] = as_h2(va.y); x.a[2] = as_h2(va.z); x.a[3] = as_h2(va.w);
       x.b[0] = as_h2(vb.x); x.b[1] = as_h2(vb.y); x.b[2] = as_h2(vb.z); x.b[3] = as_h2(vb.w);
       x.c[0] = as_h2(vc.x); x.c[1] = as_h2(vc.y); x.c[2] = as_h2(vc.z); x.c[3] = as_h2(vc.w);
       x.d[0] = as_h2(vd.x); x.d[1] = as_h2(vd.y); x.d[2] = as_h2(vd.z); x.d[3] = as_h2(vd.w);
-      x.xs8 = xsum[p.s * CP + c];
-      acc = __builtin_fmaf(chunk_dot(b.w[j], x), decode_scale(b.q[j], a.sdt), acc);
+      x.xs8 = xsum[q.s * CT + c];
+      const float t = __builtin_fmaf(chunk_dot(b.w[j], x), decode_scale(b.q[j], a.sdt), acc);
+      acc = (ONE || c0 < cpr) ? t : acc;  // one pass: x is zero past cpr
     }
-    float dsum = row16_sum(acc) * kTwo24;
-    if (a.round_f16) dsum = (float)(half_t)dsum;
-    const float w = p.s < top_k ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), p.s))
-                                : 1.0f;
-    const float next = add_mul_rn(o, w, dsum);  // weighted_accumulate_f32 in slot order
-    o = keep ? next : o;                         // (engine.rs:5262-5302)
+    if (q.p == P - 1) {  // the slot's last pass: its row sums, rounded, into the combine
+      float dsum = lanes_sum<L>(acc) * kTwo24;
+      if (a.round_f16) dsum = (float)(half_t)dsum;
+      const float w =
+          q.s < top_k ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), q.s))
+                      : 1.0f;
+      const float next = add_mul_rn(o, w, dsum);  // weighted_accumulate_f32 in slot order
+      o = keep ? next : o;                         // (engine.rs:5262-5302)
+      acc = 0.0f;
+    }
   };
 
-  // NB load buffers in a ring: while batch i is reduced, batches i+1 .. i+NB-1 are loading
+  // NB load buffers in a ring: while batch i is reduced, batch i+1 is loading
   DownRowsBatch<J> buf[NB];
   Pos pos[NB];
-  pos[0] = Pos{g0, 0};
+  pos[0] = Pos{0, 0};
 #pragma unroll
   for (int b = 1; b < NB; b++) pos[b] = advance(pos[b - 1]);
   VIB3_TRACE_POINT(1);
   // stage the activations: each thread takes up to three chunks per pass and issues all of
   // their loads before converting any (one round trip per pass, not one per chunk)
   const char* hb = (const char*)a.h;
-  const int nitem = ns * CP, bd = (int)blockDim.x;
+  const int nitem = ns * CT, bd = (int)blockDim.x;
   auto load_raw = [&](int i0, uint4 (&raw)[3][4]) {
 #pragma unroll
     for (int u = 0; u < 3; u++) {
       const int i = min(i0 + u * bd, nitem - 1);
-      const int sl = i / CP, c = min(i - sl * CP, cpr - 1);
+      const int sl = i / CT, c = min(i - sl * CT, cpr - 1);
       const uint4* src = (const uint4*)(hb + ((size_t)sl * a.K + (size_t)c * 32) * 2);
 #pragma unroll
       for (int q = 0; q < 4; q++) raw[u][q] = src[q];
@@ -728,33 +748,30 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
     for (int u = 0; u < 3; u++) {
       const int i = i0 + u * bd;
       if (i >= nitem) break;
-      const int sl = i / CP, c = i - sl * CP;
+      const int sl = i / CT, c = i - sl * CT;
       XChunk hi, lo;
-      if (c < cpr) {
-        float xv[32];
+      float xv[32];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const uint32_t w[4] = {raw[u][q].x, raw[u][q].y, raw[u][q].z, raw[u][q].w};
+      for (int q = 0; q < 4; q++) {
+        const uint32_t w[4] = {raw[u][q].x, raw[u][q].y, raw[u][q].z, raw[u][q].w};
 #pragma unroll
-          for (int j = 0; j < 4; j++) {
-            xv[8 * q + 2 * j] = f16_to_f32((uint16_t)(w[j] & 0xffff));
-            xv[8 * q + 2 * j + 1] = f16_to_f32((uint16_t)(w[j] >> 16));
-          }
+        for (int j = 0; j < 4; j++) {
+          xv[8 * q + 2 * j] = f16_to_f32((uint16_t)(w[j] & 0xffff));
+          xv[8 * q + 2 * j + 1] = f16_to_f32((uint16_t)(w[j] >> 16));
         }
-        make_chunk(xv, hi, lo);
-      } else {
-        zero_chunk(hi);
       }
-      uint4* xp = xq + (size_t)sl * 4 * CP + c;
+      if (c < cpr) make_chunk(xv, hi, lo);
+      else zero_chunk(hi);
+      uint4* xp = xq + (size_t)sl * 4 * CT + c;
       auto pack = [](const h2 (&v)[4]) {
         return make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
                           __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
       };
       xp[0] = pack(hi.a);
-      xp[CP] = pack(hi.b);
-      xp[2 * CP] = pack(hi.c);
-      xp[3 * CP] = pack(hi.d);
-      xsum[sl * CP + c] = hi.xs8;
+      xp[CT] = pack(hi.b);
+      xp[2 * CT] = pack(hi.c);
+      xp[3 * CT] = pack(hi.d);
+      xsum[sl * CT + c] = hi.xs8;
     }
   };
   {
@@ -795,7 +812,7 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
   }
   // stored after the loop: a store inside it would share the load counter with the weight
   // loads, and the compiler then waits for all of them at the loop head
-  const int r = 4 * g0 + grp;
+  const int r = R * g0 + grp;
   if (sub == 0 && r < a.M) a.out[r] = o;
   VIB3_TRACE_POINT(3);
 }
@@ -957,32 +974,49 @@ static void launch_down_t(DownArgs& a, hipStream_t s, KTime t) {
 #endif
 constexpr int kDownRowsBuffers = VIB3_DOWN_ROWS_BUFFERS;
 
-// LDS bytes of k_down_rows: per slot, 16 * J chunks of 4 pair words and one offset term.
-static size_t down_rows_lds(int nslots, int J) { return (size_t)nslots * 16 * J * (64 + 4); }
+// LDS bytes of k_down_rows: per slot, every chunk's 4 pair words and one offset term.
+static size_t down_rows_lds(int nslots, int chunks) {
+  return (size_t)nslots * chunks * (64 + 4);
+}
 
-template <int J>
+template <int R, int J, bool ONE>
 static void launch_down_rows_t(DownArgs& a, hipStream_t s, KTime t) {
   // One row group per wave, and as many waves per workgroup as make one workgroup per CU
   // (2..8): every CU streams the same share of the weights, and stages the activations once.
   // (Four-wave workgroups left some CUs two workgroups and others one.)
-  const int groups = (a.M + 3) / 4;
+  const int groups = (a.M + R - 1) / R;
   int wpb = env_int("VIB3_DOWN_WAVES", (groups + device_cus() - 1) / device_cus());
   wpb = wpb < 2 ? 2 : wpb > 8 ? 8 : wpb;
   const int blocks = (groups + wpb - 1) / wpb;
-  hipExtLaunchKernelGGL((k_down_rows<J, kDownRowsBuffers>), dim3((unsigned)blocks), dim3(64 * wpb),
-                        (unsigned)down_rows_lds(a.nslots, J), s, t.start, t.stop, 0, a);
+  const int chunks = ONE ? kWave / R * J : a.K / 32;
+  hipExtLaunchKernelGGL((k_down_rows<R, J, kDownRowsBuffers, ONE>), dim3((unsigned)blocks),
+                        dim3(64 * wpb), (unsigned)down_rows_lds(a.nslots, chunks), s, t.start,
+                        t.stop, 0, a);
+}
+
+template <int R>
+static void launch_down_rows_j(DownArgs& a, int cpr, hipStream_t s, KTime t) {
+  constexpr int L = kWave / R;  // J: chunks per lane per pass, enough for one pass up to 4
+  if (cpr <= L) launch_down_rows_t<R, 1, true>(a, s, t);
+  else if (cpr <= 2 * L) launch_down_rows_t<R, 2, true>(a, s, t);
+  else if (cpr <= 4 * L) launch_down_rows_t<R, 4, true>(a, s, t);
+  else launch_down_rows_t<R, 4, false>(a, s, t);
 }
 
 int launch_down(DownArgs a, hipStream_t s, KTime t) {
   const int cpr = a.K / 32;
   if (a.M <= 0) return 0;
-  // staged-activation kernel for f16 intermediates of up to 64 chunks per row
-  const int J = cpr <= 16 ? 1 : cpr <= 32 ? 2 : cpr <= 64 ? 4 : 0;
-  if (a.h_dt == VIB3_DT_F16 && J && down_rows_lds(a.nslots, J) <= 64 * 1024 &&
+  // staged-activation kernel for f16 intermediates whose staged form fits 64 KB of LDS;
+  // rows per wave: 4 while that leaves enough row groups to fill the GPU, else 2 or 1
+  const int waves = 6 * device_cus();
+  const int R = a.M / 4 >= waves ? 4 : a.M / 2 >= waves ? 2 : 1;
+  const int L = kWave / R;  // the LDS holds one pass's chunks (padded) or all cpr
+  const int chunks = cpr <= L ? L : cpr <= 2 * L ? 2 * L : cpr <= 4 * L ? 4 * L : cpr;
+  if (a.h_dt == VIB3_DT_F16 && down_rows_lds(a.nslots, chunks) <= 64 * 1024 &&
       env_int("VIB3_DOWN_COMBINE", 0) == 0) {
-    if (J == 1) launch_down_rows_t<1>(a, s, t);
-    else if (J == 2) launch_down_rows_t<2>(a, s, t);
-    else launch_down_rows_t<4>(a, s, t);
+    if (R == 4) launch_down_rows_j<4>(a, cpr, s, t);
+    else if (R == 2) launch_down_rows_j<2>(a, cpr, s, t);
+    else launch_down_rows_j<1>(a, cpr, s, t);
     VIB3_RETURN_LAUNCH();
   }
   const int ks = (cpr + kDownSpan - 1) / kDownSpan;
