@@ -749,29 +749,35 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
       const int i = i0 + u * bd;
       if (i >= nitem) break;
       const int sl = i / CT, c = i - sl * CT;
-      XChunk hi, lo;
-      float xv[32];
+      // f16 intermediates are already f16 pairs: the pair layout is a permutation of the
+      // words ((x0,x4) (x1,x5) (x2,x6) (x3,x7) of each 8), and the offset term the sum of
+      // the 32 values in index order (make_chunk's numbers exactly, without its conversions)
+      uint32_t A[4], B[4], C[4], D[4];
+      float sum = 0.0f;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const uint32_t w[4] = {raw[u][q].x, raw[u][q].y, raw[u][q].z, raw[u][q].w};
+        A[q] = (w[0] & 0xffffu) | (w[2] << 16);
+        B[q] = (w[0] >> 16) | (w[2] & 0xffff0000u);
+        C[q] = (w[1] & 0xffffu) | (w[3] << 16);
+        D[q] = (w[1] >> 16) | (w[3] & 0xffff0000u);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          xv[8 * q + 2 * j] = f16_to_f32((uint16_t)(w[j] & 0xffff));
-          xv[8 * q + 2 * j + 1] = f16_to_f32((uint16_t)(w[j] >> 16));
+          sum += f16_to_f32((uint16_t)(w[j] & 0xffff));
+          sum += f16_to_f32((uint16_t)(w[j] >> 16));
         }
       }
-      if (c < cpr) make_chunk(xv, hi, lo);
-      else zero_chunk(hi);
-      uint4* xp = xq + (size_t)sl * 4 * CT + c;
-      auto pack = [](const h2 (&v)[4]) {
-        return make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
-                          __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
+      const bool in = c < cpr;  // (selected word by word: a select of whole vectors went
+                                // through scratch memory)
+      auto word4 = [&](const uint32_t (&v)[4]) {
+        return make_uint4(in ? v[0] : 0u, in ? v[1] : 0u, in ? v[2] : 0u, in ? v[3] : 0u);
       };
-      xp[0] = pack(hi.a);
-      xp[CT] = pack(hi.b);
-      xp[2 * CT] = pack(hi.c);
-      xp[3 * CT] = pack(hi.d);
-      xsum[sl * CT + c] = hi.xs8;
+      uint4* xp = xq + (size_t)sl * 4 * CT + c;
+      xp[0] = word4(A);
+      xp[CT] = word4(B);
+      xp[2 * CT] = word4(C);
+      xp[3 * CT] = word4(D);
+      xsum[sl * CT + c] = in ? 8.0f * kTwoM24 * sum : 0.0f;
     }
   };
   {
