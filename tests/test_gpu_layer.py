@@ -167,6 +167,28 @@ def test_small_layer_two_shared(layout, tile):
                 normalize=False)
 
 
+@pytest.mark.parametrize("hidden,inter,group,tile", [
+    (7168, 4096, 32, 0),     # 4 rows per wave, k in two passes
+    (1024, 9216, 64, 0),     # 1 row per wave, k in two passes (288 chunks of 32)
+    (1536, 9600, 96, 48),    # 1 row per wave, two passes, group 96, 48-row pages
+])
+def test_down_multipass_shapes(hidden, inter, group, tile):
+    """Down shapes whose k needs several passes of the staged-activation kernel, with a
+    group size that is not a power of two and paged rows."""
+    from vib3_amd import moe
+    from vib3_amd._lib import DT_BF16, ROUTER_SOFTMAX
+    _say(f"case: down multipass hidden={hidden} inter={inter} g={group} tile={tile}")
+    shape = moe.BankShape(hidden=hidden, inter=inter, group_size=group, scale_dtype=DT_BF16,
+                          scale_sigma=0.02, num_experts=4, num_shared=1)
+    layout = "paged" if tile else "contiguous"
+    bank = moe.Int4ExpertBank(shape, layer=5, seed=SEED, layout=layout, tile_rows=tile or 64,
+                              pool_bytes=256 << 20 if tile else None)
+    w, _ = moe.make_router(shape, 5, SEED, 0.02, None)
+    layer = moe.MoeInt4Layer(bank, w, None, top_k=2, scoring_mode=ROUTER_SOFTMAX)
+    x = moe.make_activation(shape.hidden, 1, SEED)
+    check_layer(layer, bank, x, w.cpu().numpy(), O.F32, None, 0, 1.0, 2)
+
+
 def test_ragged_rows_per_page():
     """Pages of 48/40 rows: the last page of each matrix is short (engine pages from the
     converter hold 520 / 1820 rows, convert.rs:1853-1865)."""
