@@ -21,7 +21,7 @@ _lib = None
 
 def build() -> None:
     """Compile liboracle.so from cpu_ref.c (gcc, -ffp-contract=off)."""
-    subprocess.check_call(["make", "-s", "-B", "-C", _HERE, "liboracle.so"])
+    subprocess.check_call(["make", "-s", "-B", "-C", _HERE, "all"])
 
 
 def lib() -> C.CDLL:
