@@ -863,30 +863,6 @@ __global__ __launch_bounds__(256) void k_int4_generic(GenericArgs a) {
 
 // ------------------------------------------------------------------------- host launchers
 
-// Resident workgroups per CU for a kernel at a block size, and the CU count (cached per device;
-// plain host queries, no allocation).
-static int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
-template <typename K>
-static int resident_blocks(K kernel, int block) {
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess ||
-      per_cu <= 0)
-    per_cu = 1;
-  return per_cu * device_cus();
-}
-
 static int pick_nch(int cpr, int max_ks, int& nch, int& ks) {
   for (int n : {1, 2, 4}) {
     if (cpr <= kWave * n) { nch = n; ks = 1; return 0; }

@@ -111,4 +111,29 @@ int launch_generic(GenericArgs a, bool dual, hipStream_t s);
 
 constexpr int kMaxExperts = 4096;
 
+// Resident workgroups per CU for a kernel at a block size, and the CU count (cached per device;
+// plain host queries, no allocation).
+static inline int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+template <typename K>
+static inline int resident_blocks(K kernel, int block) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess ||
+      per_cu <= 0)
+    per_cu = 1;
+  return per_cu * device_cus();
+}
+
+
 }  // namespace vib3

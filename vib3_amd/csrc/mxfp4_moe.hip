@@ -30,11 +30,13 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kMxTokBlk = 16;            // tokens per MFMA column block
-constexpr int kMxMaxBlk = 1;             // column blocks per pass (16 tokens; more = more passes)
+constexpr int kMxTokBlk = 16;            // tokens per MFMA column block (one wave)
+constexpr int kMxMaxBlk = 1;             // column blocks per wave
+constexpr int kMxChunk = 64;             // tokens of one expert sharing a weight read (4 waves)
 constexpr int kMxStep = 256;             // k per step: 2 halves x 4 lane groups x 32
 constexpr int kMxTiles = 4;              // 16-row A tiles per wave
 constexpr int kMxMaxPicks = 4096;        // tokens * top_k per launch (grouping is one workgroup)
+constexpr int kMxColdMax = 2;            // experts with at most this many tokens take the row path
 
 struct MxArgs {
   const uint16_t* x;          // [T][hidden] bf16
@@ -44,11 +46,13 @@ struct MxArgs {
   const int* d_cnt;           // [nd] entries of d
   const int* nd;              // number of distinct experts
   const int* it_d;            // [items] distinct index of each work item
-  const int* it_p0;           // [items] first entry of the item within its expert
+  const int* it_p0;           // [items] first entry of the item's token chunk within its expert
+  const int* it_np;           // [items] token blocks of the chunk (1, 2, 4) | part << 8
   const int* nitems;
   const int* ent_tok;         // [T*top_k] token of each entry (grouped by expert)
   const int* ent_slot;        // [T*top_k] t*top_k + j of each entry
-  const uint16_t* zero;       // zero row (>= max(hidden, inter) halves)
+  const int* c_dix;           // [ncold] distinct index of each cold expert (row path)
+  const int* ncold;
   uint16_t* h;                // [T*top_k][inter] f16, by entry
   uint16_t* d;                // [T*top_k][hidden] f16, by slot
   int hidden, inter;
@@ -166,9 +170,13 @@ __device__ __forceinline__ void mx_pass(const uint8_t* const (&tcode)[kMxTiles],
   }
 }
 
+// Work item = (distinct expert, chunk of up to 64 of its tokens, part). A chunk of nb token
+// blocks (nb = 1, 2 or 4) is split into nb parts; the four waves of a workgroup cover
+// 4 / nb row tiles x nb token blocks of the part's rows. The nb waves that share rows read the
+// same weight lines at about the same time, so HBM serves each line once per chunk and the
+// other reads hit the cache; a hot expert's weights are no longer fetched once per 16 tokens.
 template <bool GATEUP>
 __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
-  // work item = (distinct expert, 16-token slice); blockIdx.x = row block of the item
   const int item = (int)blockIdx.y;
   if (item >= *a.nitems) return;
   const int lane = lane_id();
@@ -176,11 +184,15 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
   const int rr = lane & 15, g = lane >> 4;
   const int dix = a.it_d[item];
   const int e = a.d_expert[dix], o_e = a.d_off[dix], t_e = a.d_cnt[dix];
-  const int p0 = a.it_p0[item];
+  const int np = a.it_np[item];
+  const int nb = np & 255, part = np >> 8;
+  const int tb = wave & (nb - 1);
+  const int p0 = a.it_p0[item] + tb * kMxTokBlk;   // this wave's first token (entry index)
+  if (p0 >= t_e) return;                            // an empty fourth block of a 3-block chunk
   const int K = GATEUP ? a.hidden : a.inter;   // reduction
   const int M = GATEUP ? a.inter : a.hidden;   // rows of each matrix
   const int rows_per_wave = GATEUP ? 32 : 64;
-  const int r0 = ((int)blockIdx.x * 4 + wave) * rows_per_wave;
+  const int r0 = (int)blockIdx.x * 4 * rows_per_wave + (part * (4 / nb) + wave / nb) * rows_per_wave;
   if (r0 >= M) return;
   const size_t pkb = (size_t)K / 2, nsb = (size_t)K / 32;
   const uint8_t* m0 = (const uint8_t*)a.table[(size_t)e * 3 + (GATEUP ? 0 : 2)];
@@ -199,15 +211,16 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
 
   {
     const int nblk = 1;
-    // B rows of this lane's column in each block (zero row past the expert's tokens)
+    // B rows of this lane's column in each block. A column past the expert's tokens reads the
+    // block's first token (the same lines as its lane, so no extra traffic): MFMA columns are
+    // independent and those columns are never stored.
     const uint16_t* brow[kMxMaxBlk];
 #pragma unroll
     for (int b = 0; b < kMxMaxBlk; b++) {
-      const int tok = p0 + b * kMxTokBlk + rr;
-      const uint16_t* r = a.zero;
-      if (tok < t_e) {
-        r = GATEUP ? a.x + (size_t)a.ent_tok[o_e + tok] * K : a.h + (size_t)(o_e + tok) * K;
-      }
+      const int tok0 = p0 + b * kMxTokBlk;
+      const int tok = tok0 + rr < t_e ? tok0 + rr : tok0;
+      const uint16_t* r =
+          GATEUP ? a.x + (size_t)a.ent_tok[o_e + tok] * K : a.h + (size_t)(o_e + tok) * K;
       brow[b] = r + g * 32;
     }
     f32x4_t acc[kMxTiles][kMxMaxBlk];
@@ -253,6 +266,187 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
   }
 }
 
+// ----------------------------------------------------------------------------- row path
+//
+// Experts picked by at most kMxColdMax tokens (three quarters of the touched experts of a
+// Zipf-skewed batch) gain nothing from the matrix cores, whose B operand would be 16 token
+// columns of which one or two are real; their cost is streaming the weights. They run as
+// multi-token GEMVs: a wave owns a contiguous range of (cold expert, row item) pairs, so it
+// streams whole rows front to back (3.5 KB gate/up rows, 1 KB down rows) instead of 128-byte
+// pieces of 64 rows, keeps the expert's one or two activation vectors in registers for the
+// whole segment, and reduces across lanes once per row.
+//
+// Lane l holds chunks l, l + 64, ... (16 bytes = 32 codes each, one E8M0 scale per chunk);
+// a chunk past the row end reads the row's last chunk and meets zero activations. Codes are
+// decoded with v_cvt_scalef32_pk_{bf16,f16}_fp4 (exact) and multiplied into f32 with
+// v_dot2_f32_{bf16,f16}. An item is one gate/up row pair (SwiGLU in the epilogue) or four down
+// rows; the next item's loads are issued before the current one is reduced.
+
+template <bool GATEUP, int NCH, int NT>
+__device__ __forceinline__ void mx_rows_segment(const MxArgs& a, int e, int o_e, int q0, int q1) {
+  constexpr int R = GATEUP ? 2 : 4;                // row loads per item
+  const int lane = lane_id();
+  const int K = GATEUP ? a.hidden : a.inter;
+  const int M = GATEUP ? a.inter : a.hidden;
+  const int cpr = K / 32;                          // chunks per row
+  const size_t pkb = (size_t)K / 2;
+  const uint8_t* m0 = (const uint8_t*)ld_table(a.table + (size_t)e * 3 + (GATEUP ? 0 : 2));
+  const uint8_t* m1 = GATEUP ? (const uint8_t*)ld_table(a.table + (size_t)e * 3 + 1) : m0;
+  const uint8_t* s0 = m0 + (size_t)M * pkb;
+  const uint8_t* s1 = m1 + (size_t)M * pkb;
+
+  int ch[NCH];
+  bool ok[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; j++) {
+    ok[j] = lane + 64 * j < cpr;
+    ch[j] = ok[j] ? lane + 64 * j : cpr - 1;
+  }
+  // activations of the segment's tokens: chunk j of token t as 4 x 16 bytes (bf16 or f16)
+  uint4 xv[NT][NCH][4];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const uint16_t* src =
+        GATEUP ? a.x + (size_t)a.ent_tok[o_e + t] * K : a.h + (size_t)(o_e + t) * K;
+#pragma unroll
+    for (int j = 0; j < NCH; j++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint4 v = ld16(src + (size_t)ch[j] * 32 + i * 8);
+        xv[t][j][i] = ok[j] ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
+  }
+
+  struct Item {
+    uint4 w[R][NCH];
+    uint8_t sc[R][NCH];
+  };
+  auto load = [&](Item& it, int q) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int row = GATEUP ? q : 4 * q + r;
+      const uint8_t* m = GATEUP && r == 1 ? m1 : m0;
+      const uint8_t* sp = GATEUP && r == 1 ? s1 : s0;
+#pragma unroll
+      for (int j = 0; j < NCH; j++) {
+        it.w[r][j] = ld_stream(m + (size_t)row * pkb + (size_t)ch[j] * 16);
+        it.sc[r][j] = ld_u8(sp + (size_t)row * cpr + ch[j]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto finish = [&](const Item& it, int q) {
+    float acc[R][NT];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+      for (int t = 0; t < NT; t++) acc[r][t] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+      for (int j = 0; j < NCH; j++) {
+        const float scale = e8m0_scale(it.sc[r][j]);
+        const uint32_t wd[4] = {it.w[r][j].x, it.w[r][j].y, it.w[r][j].z, it.w[r][j].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          uint32_t wp[4];
+          if (GATEUP) {
+            wp[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[i], scale, 0));
+            wp[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[i], scale, 1));
+            wp[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[i], scale, 2));
+            wp[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[i], scale, 3));
+          } else {
+            wp[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], scale, 0));
+            wp[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], scale, 1));
+            wp[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], scale, 2));
+            wp[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], scale, 3));
+          }
+#pragma unroll
+          for (int t = 0; t < NT; t++) {
+            const uint32_t xw[4] = {xv[t][j][i].x, xv[t][j][i].y, xv[t][j][i].z, xv[t][j][i].w};
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+              if (GATEUP)
+                acc[r][t] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wp[p]),
+                                                            __builtin_bit_cast(bf16x2_t, xw[p]),
+                                                            acc[r][t], false);
+              else
+                acc[r][t] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, wp[p]),
+                                                   __builtin_bit_cast(f16x2_t, xw[p]), acc[r][t],
+                                                   false);
+            }
+          }
+        }
+      }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+      for (int t = 0; t < NT; t++) acc[r][t] = wave_sum(acc[r][t]);
+    if (lane < NT) {
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        if (t != lane) continue;
+        if (GATEUP) {
+          const float up = acc[0][t], gate = acc[1][t];
+          a.h[(size_t)(o_e + t) * M + q] =
+              f32_to_f16_bits((gate / (1.0f + expf(-gate))) * up);  // kernels.rs:3041
+        } else {
+          const int slot = a.ent_slot[o_e + t];
+          const uint2 v = make_uint2(
+              (uint32_t)f32_to_f16_bits(acc[0][t]) | ((uint32_t)f32_to_f16_bits(acc[1][t]) << 16),
+              (uint32_t)f32_to_f16_bits(acc[2][t]) | ((uint32_t)f32_to_f16_bits(acc[3][t]) << 16));
+          *(uint2*)(a.d + (size_t)slot * M + 4 * q) = v;
+        }
+      }
+    }
+  };
+  Item A, B;
+  const int last = q1 - 1;
+  load(A, q0);
+  for (int q = q0;; q += 2) {
+    load(B, min(q + 1, last));  // past the end: re-reads the last item (no branch)
+    finish(A, q);
+    if (q + 1 > last) break;
+    load(A, min(q + 2, last));
+    finish(B, q + 1);
+    if (q + 2 > last) break;
+  }
+}
+
+template <bool GATEUP, int NCH>
+__global__ __launch_bounds__(256) void k_mx_rows(MxArgs a) {
+  const int ncold = *a.ncold;
+  const int per = GATEUP ? a.inter : a.hidden / 4;  // items per expert
+  const long n = (long)ncold * per;
+  const int W = (int)gridDim.x * 4;
+  const int w = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const long i1 = n * (w + 1) / W;
+  for (long i = n * w / W; i < i1;) {
+    const int c = (int)(i / per);
+    const int q0 = (int)(i - (long)c * per);
+    const int q1 = (int)min((long)per, i1 - (long)c * per);
+    const int dix = a.c_dix[c];
+    const int e = a.d_expert[dix], o_e = a.d_off[dix], t_e = a.d_cnt[dix];
+    if (t_e == 1)
+      mx_rows_segment<GATEUP, NCH, 1>(a, e, o_e, q0, q1);
+    else
+      mx_rows_segment<GATEUP, NCH, 2>(a, e, o_e, q0, q1);
+    i = (long)c * per + q1;
+  }
+}
+
+// Token blocks of a chunk of c tokens (1 <= c <= 64), rounded up to a divisor of 4.
+__host__ __device__ constexpr int mx_chunk_blocks(int c) {
+  return c <= kMxTokBlk ? 1 : c <= 2 * kMxTokBlk ? 2 : 4;
+}
+
+// Work items of an expert with c entries: one per part of each 64-token chunk.
+__host__ __device__ inline int mx_expert_items(int c) {
+  int n = 0;
+  for (int p0 = 0; p0 < c; p0 += kMxChunk) n += mx_chunk_blocks(c - p0 < kMxChunk ? c - p0 : kMxChunk);
+  return n;
+}
+
 // Group the T*top_k picks by expert (one workgroup). Entries of an expert keep pick order.
 // Work items for the GEMM kernels are (distinct expert, 16-token slice of its entries).
 struct MxGroupArgs {
@@ -263,22 +457,22 @@ struct MxGroupArgs {
   int* d_cnt;
   int* nd;
   int* it_d;            // [items] distinct index of each work item
-  int* it_p0;           // [items] first entry (within the expert) of each work item
+  int* it_p0;           // [items] first entry (within the expert) of the item's chunk
+  int* it_np;           // [items] token blocks of the chunk | part << 8
   int* nitems;
   int* ent_tok;
   int* ent_slot;
-  uint16_t* zero;
-  int zero_len;
+  int* c_dix;           // [ncold] distinct index of each expert of the row path
+  int* ncold;
   int top_k;
 };
 
 __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int off[kMaxExperts];
-  __shared__ int part[1024], dpart[1024], ipart[1024];
+  __shared__ int part[1024], dpart[1024], ipart[1024], cpart[1024];
   __shared__ uint16_t sid[kMxMaxPicks];
   const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
-  for (int i = tid; i < a.zero_len; i += nt) a.zero[i] = 0;
   for (int e = tid; e < a.E; e += nt) cnt[e] = 0;
   for (int p = tid; p < a.n; p += nt) sid[p] = a.ids[p];
   __syncthreads();
@@ -290,37 +484,47 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
   // contiguous span of experts.
   const int span = (a.E + nt - 1) / nt;
   const int e0 = min(a.E, tid * span), e1 = min(a.E, e0 + span);
-  int s = 0, ds = 0, is = 0;
+  // experts with 1..kMxColdMax entries go to the row path, the others to matrix-core items
+  int s = 0, ds = 0, is = 0, cs = 0;
   for (int e = e0; e < e1; e++) {
     s += cnt[e];
     ds += cnt[e] > 0;
-    is += (cnt[e] + kMxTokBlk - 1) / kMxTokBlk;
+    is += cnt[e] > kMxColdMax ? mx_expert_items(cnt[e]) : 0;
+    cs += cnt[e] > 0 && cnt[e] <= kMxColdMax;
   }
   part[tid] = s;
   dpart[tid] = ds;
   ipart[tid] = is;
+  cpart[tid] = cs;
   __syncthreads();
   for (int st = 1; st < nt; st <<= 1) {  // Hillis-Steele inclusive scans
     const int v = tid >= st ? part[tid - st] : 0;
     const int dv = tid >= st ? dpart[tid - st] : 0;
     const int iv = tid >= st ? ipart[tid - st] : 0;
+    const int cv = tid >= st ? cpart[tid - st] : 0;
     __syncthreads();
     part[tid] += v;
     dpart[tid] += dv;
     ipart[tid] += iv;
+    cpart[tid] += cv;
     __syncthreads();
   }
-  int run = part[tid] - s, drun = dpart[tid] - ds, irun = ipart[tid] - is;
+  int run = part[tid] - s, drun = dpart[tid] - ds, irun = ipart[tid] - is, crun = cpart[tid] - cs;
   for (int e = e0; e < e1; e++) {
     off[e] = run;
+    if (cnt[e] > 0 && cnt[e] <= kMxColdMax) a.c_dix[crun++] = drun;
     if (cnt[e] > 0) {
       a.d_expert[drun] = e;
       a.d_off[drun] = run;
       a.d_cnt[drun] = cnt[e];
-      for (int p0 = 0; p0 < cnt[e]; p0 += kMxTokBlk) {
-        a.it_d[irun] = drun;
-        a.it_p0[irun] = p0;
-        irun++;
+      for (int p0 = 0; cnt[e] > kMxColdMax && p0 < cnt[e]; p0 += kMxChunk) {
+        const int nb = mx_chunk_blocks(min(kMxChunk, cnt[e] - p0));
+        for (int part = 0; part < nb; part++) {
+          a.it_d[irun] = drun;
+          a.it_p0[irun] = p0;
+          a.it_np[irun] = nb | (part << 8);
+          irun++;
+        }
       }
       drun++;
     }
@@ -329,6 +533,7 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
   if (tid == nt - 1) {
     *a.nd = dpart[nt - 1];
     *a.nitems = ipart[nt - 1];
+    *a.ncold = cpart[nt - 1];
   }
   __syncthreads();
   // entry position = expert offset + number of earlier picks of the same expert
@@ -358,14 +563,37 @@ __global__ __launch_bounds__(256) void k_mx_combine(const uint16_t* d, const flo
   out[(size_t)t * hidden + r] = f32_to_bf16_bits(o);
 }
 
+// Row-path launch: K = the reduction length picks the chunks per lane (K <= 8192).
+template <bool GATEUP>
+static void mx_launch_rows(const MxArgs& a, int K, hipStream_t st) {
+  const int nch = (K / 32 + 63) / 64;
+  auto launch = [&](auto kernel) {
+    static int grid[64] = {0};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    int& g = grid[dev & 63];
+    if (!g) g = resident_blocks(kernel, 256);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)g), dim3(256), 0, st, a);
+  };
+  switch (nch) {
+    case 1: launch(k_mx_rows<GATEUP, 1>); break;
+    case 2: launch(k_mx_rows<GATEUP, 2>); break;
+    case 3: launch(k_mx_rows<GATEUP, 3>); break;
+    default: launch(k_mx_rows<GATEUP, 4>); break;
+  }
+}
+
 struct MxWs {
-  size_t d_expert, d_off, d_cnt, nd, it_d, it_p0, nitems, ent_tok, ent_slot, zero, h, d, total;
+  size_t d_expert, d_off, d_cnt, nd, it_d, it_p0, it_np, nitems, ent_tok, ent_slot, c_dix, ncold,
+      h, d, total;
 };
 
-// Upper bound of the work items: sum over touched experts of ceil(count / 16).
+// Upper bound of the work items. A chunk of c tokens has ceil(c / 16) blocks, plus one when
+// 3 blocks round up to 4: at most n / 16 + 2 per chunk, and there are at most
+// min(E, n) + n / 64 chunks.
 static int mx_max_items(const vib3_moe_mxfp4_batch* B) {
   const int n = B->tokens * B->top_k;
-  return n / kMxTokBlk + (B->num_experts < n ? B->num_experts : n);
+  return n / kMxTokBlk + 2 * ((B->num_experts < n ? B->num_experts : n) + n / kMxChunk);
 }
 
 static MxWs mx_ws(const vib3_moe_mxfp4_batch* B) {
@@ -383,10 +611,12 @@ static MxWs mx_ws(const vib3_moe_mxfp4_batch* B) {
   w.nd = take(sizeof(int));
   w.it_d = take(sizeof(int) * (size_t)mx_max_items(B));
   w.it_p0 = take(sizeof(int) * (size_t)mx_max_items(B));
+  w.it_np = take(sizeof(int) * (size_t)mx_max_items(B));
   w.nitems = take(sizeof(int));
   w.ent_tok = take(sizeof(int) * n);
   w.ent_slot = take(sizeof(int) * n);
-  w.zero = take(2 * (size_t)(B->hidden > B->inter ? B->hidden : B->inter));
+  w.c_dix = take(sizeof(int) * B->num_experts);
+  w.ncold = take(sizeof(int));
   w.h = take(2 * n * B->inter);
   w.d = take(2 * n * B->hidden);
   w.total = o;
@@ -409,8 +639,10 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   if (B->tokens <= 0 || B->top_k <= 0 || B->num_experts <= 0 || B->num_experts > kMaxExperts)
     return VIB3_ERR_BAD_COUNT;
   if ((size_t)B->tokens * B->top_k > kMxMaxPicks) return VIB3_ERR_BAD_COUNT;
-  if (B->hidden <= 0 || B->inter <= 0 || B->hidden % 256 || B->inter % 256)
-    return VIB3_ERR_UNSUPPORTED;  // 256-wide k steps; 256 rows per down workgroup
+  if (B->hidden <= 0 || B->inter <= 0 || B->hidden % 256 || B->inter % 256 ||
+      B->hidden > 8192 || B->inter > 8192)
+    return VIB3_ERR_UNSUPPORTED;  // 256-wide k steps; 256 rows per down workgroup; row path
+                                  // holds at most 4 chunks of a row per lane
   if (!B->x || !B->ids || !B->weights || !B->page_table || !B->out || !B->workspace)
     return VIB3_ERR_BAD_POINTER;
   if (((uintptr_t)B->x & 15) || ((uintptr_t)B->workspace & 255)) return VIB3_ERR_BAD_POINTER;
@@ -425,23 +657,26 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   ga.d_expert = (int*)(ws + w.d_expert); ga.d_off = (int*)(ws + w.d_off);
   ga.d_cnt = (int*)(ws + w.d_cnt); ga.nd = (int*)(ws + w.nd);
   ga.ent_tok = (int*)(ws + w.ent_tok); ga.ent_slot = (int*)(ws + w.ent_slot);
-  ga.it_d = (int*)(ws + w.it_d); ga.it_p0 = (int*)(ws + w.it_p0); ga.nitems = (int*)(ws + w.nitems);
-  ga.zero = (uint16_t*)(ws + w.zero);
-  ga.zero_len = B->hidden > B->inter ? B->hidden : B->inter;
+  ga.it_d = (int*)(ws + w.it_d); ga.it_p0 = (int*)(ws + w.it_p0); ga.it_np = (int*)(ws + w.it_np);
+  ga.nitems = (int*)(ws + w.nitems);
+  ga.c_dix = (int*)(ws + w.c_dix); ga.ncold = (int*)(ws + w.ncold);
   ga.top_k = B->top_k;
   hipLaunchKernelGGL(k_mx_group, dim3(1), dim3(1024), 0, st, ga);
 
   MxArgs a{};
   a.x = (const uint16_t*)B->x; a.table = B->page_table;
   a.d_expert = ga.d_expert; a.d_off = ga.d_off; a.d_cnt = ga.d_cnt; a.nd = ga.nd;
-  a.it_d = ga.it_d; a.it_p0 = ga.it_p0; a.nitems = ga.nitems;
-  a.ent_tok = ga.ent_tok; a.ent_slot = ga.ent_slot; a.zero = ga.zero;
+  a.it_d = ga.it_d; a.it_p0 = ga.it_p0; a.it_np = ga.it_np; a.nitems = ga.nitems;
+  a.ent_tok = ga.ent_tok; a.ent_slot = ga.ent_slot;
+  a.c_dix = ga.c_dix; a.ncold = ga.ncold;
   a.h = (uint16_t*)(ws + w.h); a.d = (uint16_t*)(ws + w.d);
   a.hidden = B->hidden; a.inter = B->inter;
   const unsigned items = (unsigned)mx_max_items(B);
   hipLaunchKernelGGL(k_mx_gemm<true>, dim3((unsigned)(B->inter / 128), items), dim3(256), 0, st, a);
+  mx_launch_rows<true>(a, B->hidden, st);
   hipLaunchKernelGGL(k_mx_gemm<false>, dim3((unsigned)(B->hidden / 256), items), dim3(256), 0, st,
                      a);
+  mx_launch_rows<false>(a, B->inter, st);
   hipLaunchKernelGGL(k_mx_combine, dim3((unsigned)((B->hidden + 255) / 256), (unsigned)B->tokens),
                      dim3(256), 0, st, (const uint16_t*)a.d, B->weights, B->ids,
                      B->num_experts, (uint16_t*)B->out, B->hidden, B->top_k);
