@@ -113,7 +113,8 @@ struct MxStep {
 template <bool GATEUP, int NB>
 __device__ __forceinline__ void mx_pass(const uint8_t* const (&tcode)[kMxTiles],
                                         const uint8_t* const (&tscale)[kMxTiles],
-                                        const uint16_t* const (&brow)[kMxMaxBlk], int K,
+                                        const uint16_t* const (&brow)[kMxMaxBlk], int ks0,
+                                        int kstride, int nsteps,
                                         f32x4_t (&acc)[kMxTiles][kMxMaxBlk]) {
   auto load = [&](MxStep<NB>& st, int ks) {
 #pragma unroll
@@ -157,26 +158,33 @@ __device__ __forceinline__ void mx_pass(const uint8_t* const (&tcode)[kMxTiles],
       }
     }
   };
+  if (nsteps <= 0) return;
   MxStep<NB> A, B;
-  const int last = K - kMxStep;
-  load(A, 0);
-  for (int ks = 0;; ks += 2 * kMxStep) {
-    load(B, min(ks + kMxStep, last));  // past the end: re-reads the last step (no branch)
+  const int last = nsteps - 1;
+  load(A, ks0);
+  for (int i = 0;; i += 2) {
+    load(B, ks0 + min(i + 1, last) * kstride);  // past the end: re-reads the last step
     compute(A);
-    if (ks + kMxStep >= K) break;
-    load(A, min(ks + 2 * kMxStep, last));
+    if (i + 1 > last) break;
+    load(A, ks0 + min(i + 2, last) * kstride);
     compute(B);
-    if (ks + 2 * kMxStep >= K) break;
+    if (i + 2 > last) break;
   }
 }
 
-// Work item = (distinct expert, chunk of up to 64 of its tokens, part). A chunk of nb token
-// blocks (nb = 1, 2 or 4) is split into nb parts; the four waves of a workgroup cover
-// 4 / nb row tiles x nb token blocks of the part's rows. The nb waves that share rows read the
-// same weight lines at about the same time, so HBM serves each line once per chunk and the
-// other reads hit the cache; a hot expert's weights are no longer fetched once per 16 tokens.
-template <bool GATEUP>
+// Work item = (distinct expert, 16-token block of its entries); blockIdx.x = row block.
+// A wave owns 4 tiles of 16 rows (gate/up: 32 up rows and the same 32 gate rows; down: 64
+// rows) for one token block. With KS = 4 (gate/up, long k) the four waves of a workgroup share
+// their tiles and split k: wave w takes the 256-wide steps w, w + 4, ... so at any time the
+// workgroup reads four adjacent 128-byte pieces of each of its rows (512 contiguous bytes)
+// rather than one piece of each of 128 rows, and the four partial tiles are summed through
+// LDS in wave order. With KS = 1 (down, k = 2048 is only 8 steps) the waves take 4 adjacent
+// row blocks and each runs its whole k range. The token blocks of one 64-token chunk are
+// adjacent items, gridDim.x (a multiple of 8) workgroups apart: the same XCD and L2, close in
+// time, so HBM serves their shared weight lines once.
+template <bool GATEUP, int KS>
 __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
+  __shared__ f32x4_t red[KS > 1 ? KS : 1][kMxTiles][kWave];
   const int item = (int)blockIdx.y;
   if (item >= *a.nitems) return;
   const int lane = lane_id();
@@ -184,16 +192,14 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
   const int rr = lane & 15, g = lane >> 4;
   const int dix = a.it_d[item];
   const int e = a.d_expert[dix], o_e = a.d_off[dix], t_e = a.d_cnt[dix];
-  const int np = a.it_np[item];
-  const int nb = np & 255, part = np >> 8;
-  const int tb = wave & (nb - 1);
-  const int p0 = a.it_p0[item] + tb * kMxTokBlk;   // this wave's first token (entry index)
-  if (p0 >= t_e) return;                            // an empty fourth block of a 3-block chunk
+  const int part = a.it_np[item] >> 8;
+  const int p0 = a.it_p0[item] + part * kMxTokBlk;  // the block's first token (entry index)
   const int K = GATEUP ? a.hidden : a.inter;   // reduction
   const int M = GATEUP ? a.inter : a.hidden;   // rows of each matrix
-  const int rows_per_wave = GATEUP ? 32 : 64;
-  const int r0 = (int)blockIdx.x * 4 * rows_per_wave + (part * (4 / nb) + wave / nb) * rows_per_wave;
-  if (r0 >= M) return;
+  const int rpw = GATEUP ? 32 : 64;                 // rows of each matrix per wave
+  const int kw = wave % KS;                          // this wave's share of the k steps
+  const int r0 = (int)blockIdx.x * rpw * (4 / KS) + (wave / KS) * rpw;
+  if (r0 >= M || p0 >= t_e) return;                  // uniform over the workgroup when KS > 1
   const size_t pkb = (size_t)K / 2, nsb = (size_t)K / 32;
   const uint8_t* m0 = (const uint8_t*)a.table[(size_t)e * 3 + (GATEUP ? 0 : 2)];
   const uint8_t* m1 = GATEUP ? (const uint8_t*)a.table[(size_t)e * 3 + 1] : m0;
@@ -228,7 +234,30 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
     for (int t = 0; t < kMxTiles; t++)
 #pragma unroll
       for (int b = 0; b < kMxMaxBlk; b++) acc[t][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    mx_pass<GATEUP, kMxMaxBlk>(tcode, tscale, brow, K, acc);
+    const int nsteps = K / kMxStep;
+    mx_pass<GATEUP, kMxMaxBlk>(tcode, tscale, brow, kw * kMxStep, KS * kMxStep,
+                               (nsteps - kw + KS - 1) / KS, acc);
+    // tiles this wave finishes: all of them (KS = 1), or with KS = 4 tile kw (gate/up: waves
+    // 0 and 1 finish row halves 0 and 1 from their up and gate tiles)
+    auto mine = [&](int t) { return KS == 1 || (GATEUP ? (t & 1) == kw : t == kw); };
+    if (KS > 1) {
+      // sum the waves' partial tiles in wave order
+#pragma unroll
+      for (int t = 0; t < kMxTiles; t++) red[kw][t][lane] = acc[t][0];
+      __syncthreads();
+      if (GATEUP && kw >= 2) return;
+#pragma unroll
+      for (int t = 0; t < kMxTiles; t++) {
+        if (!mine(t)) continue;
+        f32x4_t v = red[0][t][lane];
+#pragma unroll
+        for (int u = 1; u < KS; u++) {
+          const f32x4_t w = red[u][t][lane];
+          v = f32x4_t{v[0] + w[0], v[1] + w[1], v[2] + w[2], v[3] + w[3]};
+        }
+        acc[t][0] = v;
+      }
+    }
 
     // epilogue: lane holds rows (g*4 + i) of each tile for token column rr of each block
 #pragma unroll
@@ -238,6 +267,7 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
       if (GATEUP) {
 #pragma unroll
         for (int half = 0; half < 2; half++) {
+          if (!mine(half)) continue;
           uint16_t hv[4];
 #pragma unroll
           for (int i = 0; i < 4; i++) {
@@ -253,6 +283,7 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
         const int slot = a.ent_slot[o_e + tok];
 #pragma unroll
         for (int t = 0; t < kMxTiles; t++) {
+          if (!mine(t)) continue;
           uint16_t dv[4];
 #pragma unroll
           for (int i = 0; i < 4; i++) dv[i] = f32_to_f16_bits(acc[t][b][i]);
@@ -672,9 +703,10 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   a.h = (uint16_t*)(ws + w.h); a.d = (uint16_t*)(ws + w.d);
   a.hidden = B->hidden; a.inter = B->inter;
   const unsigned items = (unsigned)mx_max_items(B);
-  hipLaunchKernelGGL(k_mx_gemm<true>, dim3((unsigned)(B->inter / 128), items), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((k_mx_gemm<true, 4>), dim3((unsigned)(B->inter / 32), items), dim3(256), 0, st,
+                     a);
   mx_launch_rows<true>(a, B->hidden, st);
-  hipLaunchKernelGGL(k_mx_gemm<false>, dim3((unsigned)(B->hidden / 256), items), dim3(256), 0, st,
+  hipLaunchKernelGGL((k_mx_gemm<false, 1>), dim3((unsigned)(B->hidden / 256), items), dim3(256), 0, st,
                      a);
   mx_launch_rows<false>(a, B->inter, st);
   hipLaunchKernelGGL(k_mx_combine, dim3((unsigned)((B->hidden + 255) / 256), (unsigned)B->tokens),
