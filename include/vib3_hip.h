@@ -93,6 +93,25 @@ int vib3_launch_router_topk(const void *hidden_state, const void *router_weights
                             float *out_weights, int hidden_dim, int num_experts, int top_k,
                             int scoring_mode, float scaling_factor, void *stream);
 
+/* cuda_ffi.rs:292 (kernels.cu:921, :1178): out_f32[d] = x[d] * inv_rms * f32(w_f16[d]),
+ * inv_rms = 1 / sqrt(sum(x^2) / dim + eps), x f32 (the pre-MoE norm, engine.rs:5072). */
+int vib3_launch_rms_norm_f32(const void *input, void *output, const void *weight, int hidden_dim,
+                             float eps, void *stream);
+
+/* cuda_ffi.rs:302 (kernels.cu:959): the same, output rounded to f16. */
+int vib3_launch_rms_norm_f32_to_f16(const void *input, void *output, const void *weight,
+                                    int hidden_dim, float eps, void *stream);
+
+/* cuda_ffi.rs:260 (kernels.cu:817, :1132): accumulator_f32[i] += layer_output_f32[i] (the
+ * residual add after the MoE sublayer, engine.rs:5302). */
+int vib3_launch_residual_add_f32_f32(void *accumulator, const void *layer_output, int dim,
+                                     void *stream);
+
+/* cuda_ffi.rs:233 (kernels.cu:2106): out_f32[i] += sigmoid(gate_dev[0]) * f32(expert_f16[i])
+ * (the shared expert's sigmoid gate, engine.rs:6392-6425). */
+int vib3_launch_sigmoid_gated_accumulate_f32(void *output, const void *expert_output,
+                                             const void *gate_dev, int dim, void *stream);
+
 /* ------------------------------------------------------------------------------------------
  * Additive launchers (no counterpart in cuda_ffi.rs): explicit dtypes, page layout, group
  * size and scale dtype, so one library serves the CPU-fallback semantics (BF16 scales,
@@ -171,6 +190,16 @@ typedef struct vib3_moe_int4_layer {
     float *out_scores;    /* [num_experts] raw logits or NULL */
     void *workspace;      /* vib3_moe_int4_workspace_bytes() bytes of scratch */
     size_t workspace_bytes;
+    /* Either side of the sublayer (engine.rs:5064-5307); zero-initialised fields leave the
+     * layer as above. norm_weight (f16 [hidden]): x is the f32 residual stream and the router
+     * and experts read RMSNorm(x) (vib3_launch_rms_norm_f32's arithmetic, norm_eps).
+     * residual (f32 [hidden]): out = residual + sublayer (may alias out).
+     * shared_gate (f16 [num_shared][hidden]): shared expert s is weighted by
+     * sigmoid(x_normed . shared_gate[s]) instead of 1.0 (engine.rs:6392-6425). */
+    const void *norm_weight;
+    float norm_eps;
+    const float *residual;
+    const void *shared_gate;
 } vib3_moe_int4_layer;
 
 /* Workspace bytes for `layer`. Zero a new workspace once before its first launch

@@ -425,17 +425,72 @@ static void run_expert(const float *x, size_t hidden, size_t inter, size_t g, in
     free(tmp);
 }
 
+void v3o_moe_layer_w(const float *x, size_t hidden, size_t inter, size_t g, int scale_dt,
+                     const v3o_expert *routed, const uint16_t *ids, const float *weights,
+                     size_t top_k, const v3o_expert *shared, size_t n_shared,
+                     const float *shared_w, int faithful, float *out, int nthreads)
+{
+    memset(out, 0, sizeof(float) * hidden); /* layer_output_buf.zero_async, engine.rs:5200 */
+    for (size_t j = 0; j < top_k; j++)
+        run_expert(x, hidden, inter, g, scale_dt, &routed[ids[j]], weights[j], faithful, out, nthreads);
+    /* shared experts: weight 1.0 (weighted_accumulate_f32, engine.rs:6441-6449) or the sigmoid
+     * of the gate (sigmoid_gated_accumulate_f32, engine.rs:6418-6424) */
+    for (size_t s = 0; s < n_shared; s++)
+        run_expert(x, hidden, inter, g, scale_dt, &shared[s], shared_w ? shared_w[s] : 1.0f,
+                   faithful, out, nthreads);
+}
+
 void v3o_moe_layer(const float *x, size_t hidden, size_t inter, size_t g, int scale_dt,
                    const v3o_expert *routed, const uint16_t *ids, const float *weights,
                    size_t top_k, const v3o_expert *shared, size_t n_shared, int faithful,
                    float *out, int nthreads)
 {
-    memset(out, 0, sizeof(float) * hidden); /* layer_output_buf.zero_async, engine.rs:5200 */
-    for (size_t j = 0; j < top_k; j++)
-        run_expert(x, hidden, inter, g, scale_dt, &routed[ids[j]], weights[j], faithful, out, nthreads);
-    for (size_t s = 0; s < n_shared; s++)
-        run_expert(x, hidden, inter, g, scale_dt, &shared[s], 1.0f, faithful, out, nthreads);
+    v3o_moe_layer_w(x, hidden, inter, g, scale_dt, routed, ids, weights, top_k, shared, n_shared,
+                    NULL, faithful, out, nthreads);
 }
+
+/* ------------------------------------------------------------------ either side of the MoE */
+
+/* vib3_rms_norm_f32 (kernels.cu:921-955): 256 strided partial sums of squares (the CUDA
+ * compiler contracts `partial_ss += val * val` into a fused multiply-add), a halving tree over
+ * the 256 partials, rms = sqrtf(ss / n + eps), inv = 1 / rms, y = (x * inv) * w. */
+float v3o_inv_rms(const float *x, size_t n, float eps)
+{
+    float part[256];
+    for (size_t t = 0; t < 256; t++) {
+        float p = 0.0f;
+        for (size_t d = t; d < n; d += 256) p = fmaf(x[d], x[d], p);
+        part[t] = p;
+    }
+    for (size_t s = 128; s > 0; s >>= 1)
+        for (size_t t = 0; t < s; t++) part[t] = part[t] + part[t + s];
+    float rms = sqrtf(part[0] / (float)n + eps);
+    return 1.0f / rms;
+}
+
+void v3o_rms_norm_f32(const float *x, size_t n, const uint16_t *w_f16, float eps, float *out)
+{
+    float inv = v3o_inv_rms(x, n, eps);
+    for (size_t d = 0; d < n; d++) out[d] = x[d] * inv * v3o_f16_to_f32(w_f16[d]);
+}
+
+/* vib3_residual_add_f32_f32_kernel (kernels.cu:817): acc[i] += lo[i]. */
+void v3o_residual_add_f32(float *acc, const float *lo, size_t n)
+{
+    for (size_t i = 0; i < n; i++) acc[i] = acc[i] + lo[i];
+}
+
+/* linear_projection_f32_to_f32 CPU body (kernels.rs:3630-3640): one output row, sequential
+ * acc += x[d] * f32(w[d]); used for the shared expert's gate logit (engine.rs:6396). */
+float v3o_linear_row_f16(const float *x, const uint16_t *w_f16, size_t n)
+{
+    float acc = 0.0f;
+    for (size_t d = 0; d < n; d++) acc += x[d] * v3o_f16_to_f32(w_f16[d]);
+    return acc;
+}
+
+/* the gate's sigmoid (kernels.cu:2114): 1 / (1 + exp(-g)) */
+float v3o_sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
 
 /* ------------------------------------------------------------------ MXFP4 */
 

@@ -15,6 +15,10 @@
  *   v3o_dequantize_int4      <- src/compute/kernels.rs:3866-3927 (dequantize_int4_to_f32)
  *   v3o_moe_layer            <- src/runtime/engine.rs:5801-6306 (execute_expert),
  *                               :6317-6456 (execute_shared_expert, weight 1.0 without gate)
+ *   v3o_moe_layer_w          <- the same with the shared expert's sigmoid gate, engine.rs:6392-6451
+ *   v3o_rms_norm_f32         <- cuda/src/kernels.cu:921-955 (vib3_rms_norm_f32; no CPU body exists)
+ *   v3o_residual_add_f32     <- cuda/src/kernels.cu:817 (vib3_residual_add_f32_f32_kernel)
+ *   v3o_linear_row_f16       <- src/compute/kernels.rs:3630-3640 (linear_projection_f32_to_f32)
  *   v3o_mxfp4_*              <- cuda/src/kernels.cu:438-441 (E2M1 table), :2770-2777 (E8M0)
  *   v3o_synth_*              synthetic-data generator spec shared with vib3_amd/csrc/synth.hip
  *
@@ -111,6 +115,20 @@ void v3o_moe_layer(const float *x, size_t hidden, size_t inter, size_t g, int sc
                    const v3o_expert *routed, const uint16_t *ids, const float *weights,
                    size_t top_k, const v3o_expert *shared, size_t n_shared, int faithful,
                    float *out, int nthreads);
+
+/* The same with the shared experts weighted by shared_w[s] (NULL: 1.0). */
+void v3o_moe_layer_w(const float *x, size_t hidden, size_t inter, size_t g, int scale_dt,
+                     const v3o_expert *routed, const uint16_t *ids, const float *weights,
+                     size_t top_k, const v3o_expert *shared, size_t n_shared,
+                     const float *shared_w, int faithful, float *out, int nthreads);
+
+/* Either side of the sublayer: RMSNorm (kernels.cu:921), residual add (kernels.cu:817),
+ * the shared-expert gate logit (kernels.rs:3630) and its sigmoid (kernels.cu:2114). */
+float v3o_inv_rms(const float *x, size_t n, float eps);
+void v3o_rms_norm_f32(const float *x, size_t n, const uint16_t *w_f16, float eps, float *out);
+void v3o_residual_add_f32(float *acc, const float *lo, size_t n);
+float v3o_linear_row_f16(const float *x, const uint16_t *w_f16, size_t n);
+float v3o_sigmoid(float g);
 
 /* MXFP4: E2M1 code (low nibble = even k) times E8M0 scale 2^(e-127) per 32 along k. */
 float v3o_e2m1(uint8_t code);

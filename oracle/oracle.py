@@ -51,6 +51,12 @@ def _declare(L: C.CDLL) -> None:
         "v3o_quantize_int4": (None, [P, S, S, S, P]),
         "v3o_dequantize_int4": (None, [P, S, S, S, I, P]),
         "v3o_moe_layer": (None, [P, S, S, S, I, P, P, P, S, P, S, I, P, I]),
+        "v3o_moe_layer_w": (None, [P, S, S, S, I, P, P, P, S, P, S, P, I, P, I]),
+        "v3o_inv_rms": (F, [P, S, F]),
+        "v3o_rms_norm_f32": (None, [P, S, P, F, P]),
+        "v3o_residual_add_f32": (None, [P, P, S]),
+        "v3o_linear_row_f16": (F, [P, P, S]),
+        "v3o_sigmoid": (F, [F]),
         "v3o_e2m1": (F, [C.c_uint8]),
         "v3o_e8m0": (F, [C.c_uint8]),
         "v3o_matmul_mxfp4_acc": (None, [P, P, P, S, S, P, I]),
@@ -200,11 +206,11 @@ def _expert_struct(pages_by_seg, rows_by_seg, keep):
 
 
 def moe_layer(x, hidden, inter, g, scale_dt, routed, ids, weights, shared, faithful=True,
-              nthreads=0) -> np.ndarray:
+              nthreads=0, shared_weights=None) -> np.ndarray:
     """engine.rs:5801 execute_expert x k + :6317 execute_shared_expert, summed in f32.
 
     routed: dict expert_id -> (pages_by_seg, rows_by_seg); only ids need to be present.
-    shared: list of (pages_by_seg, rows_by_seg)."""
+    shared: list of (pages_by_seg, rows_by_seg); shared_weights: their gates (None: 1.0)."""
     keep = []
     x = np.ascontiguousarray(x, dtype=np.float32)
     ids = np.ascontiguousarray(ids, dtype=np.uint16)
@@ -218,10 +224,44 @@ def moe_layer(x, hidden, inter, g, scale_dt, routed, ids, weights, shared, faith
     for s, (pages, rows) in enumerate(shared):
         sh[s] = _expert_struct(pages, rows, keep)
     out = np.empty(hidden, dtype=np.float32)
-    lib().v3o_moe_layer(_p(x), hidden, inter, g, scale_dt, C.cast(arr, C.c_void_p), _p(ids),
-                        _p(weights), ids.size, C.cast(sh, C.c_void_p), len(shared),
-                        int(bool(faithful)), _p(out), nthreads)
+    sw = None if shared_weights is None else np.ascontiguousarray(shared_weights, np.float32)
+    lib().v3o_moe_layer_w(_p(x), hidden, inter, g, scale_dt, C.cast(arr, C.c_void_p), _p(ids),
+                          _p(weights), ids.size, C.cast(sh, C.c_void_p), len(shared),
+                          None if sw is None else _p(sw), int(bool(faithful)), _p(out), nthreads)
     return out
+
+
+# ---------------------------------------------------------------- either side of the MoE
+
+def inv_rms(x, eps) -> float:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return lib().v3o_inv_rms(_p(x), x.size, float(eps))
+
+
+def rms_norm_f32(x, w_f16_bits, eps) -> np.ndarray:
+    """vib3_rms_norm_f32 (kernels.cu:921): (x * inv_rms) * f32(w), x f32, w f16 bits."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w_f16_bits, dtype=np.uint16)
+    out = np.empty_like(x)
+    lib().v3o_rms_norm_f32(_p(x), x.size, _p(w), float(eps), _p(out))
+    return out
+
+
+def residual_add_f32(acc, lo) -> np.ndarray:
+    out = np.array(acc, dtype=np.float32, copy=True)
+    lo = np.ascontiguousarray(lo, dtype=np.float32)
+    lib().v3o_residual_add_f32(_p(out), _p(lo), out.size)
+    return out
+
+
+def linear_row_f16(x, w_f16_bits) -> float:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w_f16_bits, dtype=np.uint16)
+    return lib().v3o_linear_row_f16(_p(x), _p(w), x.size)
+
+
+def sigmoid(g) -> float:
+    return lib().v3o_sigmoid(float(g))
 
 
 def e2m1(code: int) -> float:

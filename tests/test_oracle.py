@@ -242,9 +242,11 @@ def test_router_softmax_equals_full_softmax_renormalised():
 
 # ---------------------------------------------------------------- layer composition
 
-def test_moe_layer_matches_dense_f64():
+@pytest.mark.parametrize("sw", [None, 0.25])
+def test_moe_layer_matches_dense_f64(sw):
     """validation.rs:122 forward_moe semantics (dense SwiGLU experts, weighted sum) in f64 on the
-    decoded weights, with multi-page experts (rows split over pages)."""
+    decoded weights, with multi-page experts (rows split over pages); sw: the shared expert's
+    sigmoid-gate weight (engine.rs:6418), None for the ungated weight 1.0."""
     rng = np.random.default_rng(9)
     hidden, inter, g, E = 128, 64, 32, 6
     x = rng.normal(0, 1, hidden).astype(np.float32)
@@ -271,10 +273,11 @@ def test_moe_layer_matches_dense_f64():
     shared = make_expert(64, 128)
     ids = np.array([4, 1], dtype=np.uint16)
     wts = np.array([0.7, 0.3], dtype=np.float32)
+    shw = None if sw is None else [sw]
     got = O.moe_layer(x, hidden, inter, g, O.BF16, {i: experts[i][0] for i in range(E)}, ids, wts,
-                      [shared[0]], faithful=False)
+                      [shared[0]], faithful=False, shared_weights=shw)
     ref = np.zeros(hidden)
-    for e, w in list(zip(ids.tolist(), wts.tolist())) + [(None, 1.0)]:
+    for e, w in list(zip(ids.tolist(), wts.tolist())) + [(None, 1.0 if sw is None else sw)]:
         m = shared[1] if e is None else experts[e][1]
         up, gate = m[0] @ x, m[1] @ x
         h = gate / (1 + np.exp(-gate)) * up
@@ -282,7 +285,7 @@ def test_moe_layer_matches_dense_f64():
     rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
     assert rel < 1e-5
     faithful = O.moe_layer(x, hidden, inter, g, O.BF16, {i: experts[i][0] for i in range(E)}, ids,
-                           wts, [shared[0]], faithful=True)
+                           wts, [shared[0]], faithful=True, shared_weights=shw)
     rel_f = np.linalg.norm(faithful - ref) / np.linalg.norm(ref)
     assert 0 < rel_f < 1e-3  # f16 rounding of h and of each down output only
 
@@ -390,3 +393,45 @@ def test_synth_page_is_layout_independent():
     pk, ng = k // 2, k // g
     assert np.array_equal(part[: 16 * pk], full[8 * pk: 24 * pk])
     assert np.array_equal(part[16 * pk:], full[rows * pk + 8 * ng * 2: rows * pk + 24 * ng * 2])
+
+
+# ---------------------------------------------------------------- either side of the MoE
+
+def test_kat_rms_norm():
+    """integration_test.rs:701 test_rms_norm: [1,2,3,4], unit weights, eps 1e-6 ->
+    x / sqrt(7.5 + eps); and :738 (unit weights) [3,4,0,0] -> [1.2, 1.6, 0, 0]."""
+    one = np.full(4, 1.0, np.float16).view(np.uint16)
+    y = O.rms_norm_f32(np.array([1, 2, 3, 4], np.float32), one, 1e-6)
+    rms = np.sqrt(np.float32(7.5) + np.float32(1e-6))
+    assert np.all(np.abs(y - np.array([1, 2, 3, 4]) / rms) < 0.01)
+    y = O.rms_norm_f32(np.array([3, 4, 0, 0], np.float32), one, 1e-6)
+    assert np.allclose(y, [1.2, 1.6, 0, 0], atol=0.01)
+
+
+@pytest.mark.parametrize("n,sigma,eps", [(7168, 30.0, 1e-6), (4096, 1.0, 1e-5),
+                                         (1000, 1e-4, 1e-6), (300, 1.0, 0.5)])
+def test_rms_norm_against_float64(n, sigma, eps):
+    """Closed form in float64: y = x / sqrt(mean(x^2) + eps) * w. The tiny-sigma case is
+    dominated by eps (a dropped eps or a divide by n - 1 fails it), the weights are not 1 (a
+    dropped weight fails), the last case has eps of the order of mean(x^2)."""
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * sigma).astype(np.float32)
+    w = (rng.random(n) + 0.5).astype(np.float16)
+    y = O.rms_norm_f32(x, w.view(np.uint16), eps)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt(np.mean(x64 * x64) + eps) * w.astype(np.float64)
+    assert np.max(np.abs(y - ref)) <= 4e-7 * np.max(np.abs(ref))
+
+
+def test_shared_gate_pieces():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(2048).astype(np.float32)
+    w = (rng.standard_normal(2048) * 0.02).astype(np.float16)
+    g = O.linear_row_f16(x, w.view(np.uint16))
+    assert abs(g - float(np.dot(x.astype(np.float64), w.astype(np.float64)))) < 1e-5
+    for v in (-20.0, -1.0, 0.0, 0.5, 30.0):
+        assert abs(O.sigmoid(v) - 1 / (1 + np.exp(-v))) < 1e-7
+    acc = rng.standard_normal(100).astype(np.float32)
+    lo = rng.standard_normal(100).astype(np.float32)
+    assert np.array_equal(O.residual_add_f32(acc, lo), acc + lo)
+

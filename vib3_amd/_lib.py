@@ -43,6 +43,8 @@ class MoeInt4Layer(C.Structure):
         ("max_pages", C.c_int), ("rows_per_page", C.c_int * 3), ("flags", C.c_int),
         ("out", C.c_void_p), ("out_ids", C.c_void_p), ("out_weights", C.c_void_p),
         ("out_scores", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+        ("norm_weight", C.c_void_p), ("norm_eps", C.c_float), ("residual", C.c_void_p),
+        ("shared_gate", C.c_void_p),
     ]
 
 
@@ -68,6 +70,10 @@ SIGNATURES = {
     "vib3_launch_weighted_accumulate_f32_f32": (I, [P, P, F, I, P]),
     "vib3_launch_router_gemv_f32": (I, [P, P, P, I, I, P]),
     "vib3_launch_router_topk": (I, [P, P, P, P, P, P, I, I, I, I, F, P]),
+    "vib3_launch_rms_norm_f32": (I, [P, P, P, I, F, P]),
+    "vib3_launch_rms_norm_f32_to_f16": (I, [P, P, P, I, F, P]),
+    "vib3_launch_residual_add_f32_f32": (I, [P, P, I, P]),
+    "vib3_launch_sigmoid_gated_accumulate_f32": (I, [P, P, P, I, P]),
     "vib3_launch_partial_matmul_int4_ex": (I, [P, I, P, P, I, I, I, I, I, P]),
     "vib3_launch_partial_swiglu_int4_ex": (I, [P, I, P, P, P, I, I, I, I, I, P]),
     "vib3_router_workspace_bytes": (S, [I]),

@@ -68,9 +68,9 @@ __global__ void k_zero(uint4* p16, size_t n16, uint8_t* tail, size_t ntail) {
 }
 
 // Workspace of the fused layer: [scores[E] | ids[k] | wts[k] | router slots u64[E] | error |
-// h[nslots][inter]].
+// h[nslots][inter] | xn f32[hidden] (with a norm) | shared weights f32[num_shared] (gated)].
 struct LayerWs {
-  size_t scores, ids, wts, slots, error, h, total;
+  size_t scores, ids, wts, slots, error, h, xn, shared_w, total;
 };
 
 // Routing mode of a layer call (see RowsArgs::route).
@@ -102,7 +102,9 @@ LayerWs layer_ws(const vib3_moe_int4_layer* L) {
   w.slots = round_up(w.wts + 4 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
   w.error = round_up(w.slots + 8 * (size_t)(L->num_experts > 0 ? L->num_experts : 0), 256);
   w.h = round_up(w.error + 4, 256);
-  w.total = round_up(w.h + hsz * (size_t)(nslots > 0 ? nslots : 0) * (size_t)(L->inter > 0 ? L->inter : 0), 256);
+  w.xn = round_up(w.h + hsz * (size_t)(nslots > 0 ? nslots : 0) * (size_t)(L->inter > 0 ? L->inter : 0), 256);
+  w.shared_w = round_up(w.xn + (L->norm_weight ? 4 * (size_t)(L->hidden > 0 ? L->hidden : 0) : 0), 256);
+  w.total = round_up(w.shared_w + (L->shared_gate ? 4 * (size_t)(L->num_shared > 0 ? L->num_shared : 0) : 0), 256);
   return w;
 }
 
@@ -296,11 +298,25 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
       (L->num_shared > 0 && !L->shared_page_table) || !aligned16(L->x) ||
       !aligned16(L->workspace))
     return VIB3_ERR_BAD_POINTER;
+  if (L->norm_weight && L->x_dtype != VIB3_DT_F32) return VIB3_ERR_UNSUPPORTED;  // f32 stream
+  if (L->shared_gate && L->num_shared <= 0) return VIB3_ERR_BAD_COUNT;
   const LayerWs w = layer_ws(L);
   if (L->workspace_bytes < w.total) return VIB3_ERR_WORKSPACE;
   char* ws = (char*)L->workspace;
   hipStream_t st = S(stream);
   auto run = [&](int i) { return only < 0 || only == i; };
+
+  // the activation the router and experts read: x, or RMSNorm(x) written by the prologue,
+  // which also computes the shared experts' gates (stage 0 with the router)
+  const void* xa = L->norm_weight ? (const void*)(ws + w.xn) : L->x;
+  const float* shared_w = L->shared_gate ? (const float*)(ws + w.shared_w) : nullptr;
+  if (run(0) && (L->norm_weight || L->shared_gate)) {
+    const int rc = launch_moe_prologue(L->x, L->x_dtype, (const uint16_t*)L->norm_weight,
+                                       L->norm_eps, L->hidden, (float*)(ws + w.xn),
+                                       (const uint16_t*)L->shared_gate, L->num_shared,
+                                       (float*)(ws + w.shared_w), st);
+    if (rc) return rc;
+  }
 
   const uint16_t* ids = (const uint16_t*)(ws + w.ids);
   const float* wts = (const float*)(ws + w.wts);
@@ -313,7 +329,7 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
         return VIB3_ERR_BAD_COUNT;
       if (L->scoring_mode != VIB3_ROUTER_SOFTMAX && L->scoring_mode != VIB3_ROUTER_SIGMOID)
         return VIB3_ERR_UNSUPPORTED;
-      router.x = L->x; router.x_dt = L->x_dtype; router.w = L->router_w;
+      router.x = xa; router.x_dt = L->x_dtype; router.w = L->router_w;
       router.w_dt = L->router_w_dtype; router.bias = L->router_bias; router.D = L->hidden;
       router.E = L->num_experts; router.top_k = L->top_k; router.mode = L->scoring_mode;
       router.scaling = L->scoring_mode == VIB3_ROUTER_SIGMOID ? L->scaling_factor : 1.0f;
@@ -348,7 +364,7 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
 
   const int h_dt = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? VIB3_DT_F32 : VIB3_DT_F16;
   RowsArgs a{};
-  a.x = L->x; a.x_dt = L->x_dtype; a.K = L->hidden; a.M = L->inter; a.g = L->group_size;
+  a.x = xa; a.x_dt = L->x_dtype; a.K = L->hidden; a.M = L->inter; a.g = L->group_size;
   a.sdt = L->scale_dtype; a.nslots = nslots;
   a.routed_table = L->page_table; a.shared_table = L->shared_page_table; a.ids = ids;
   a.top_k = L->top_k; a.max_pages = L->max_pages;
@@ -372,6 +388,8 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
   d.magic = page_magic(L->rows_per_page[2]);
   d.round_f16 = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? 0 : 1;
   d.out = L->out;
+  d.residual = L->residual;
+  d.shared_w = shared_w;
   return run(2) ? launch_down(d, st) : 0;
 }
 

@@ -507,7 +507,9 @@ __global__ __launch_bounds__(WIDE ? 1024 : 640) void k_down_combine(DownArgs a) 
   };
   // router weights: lane s holds slot s's (read once; a load at each block's combine would
   // wait for every weight load in flight)
-  const float my_w = lane < a.top_k ? a.wts[lane] : 0.f;
+  const float my_w = lane < a.top_k    ? a.wts[lane]
+                     : lane < a.nslots ? (a.shared_w ? a.shared_w[lane - a.top_k] : 1.0f)
+                                       : 0.f;
   XChunk xh[kDownJ], xl[kDownJ];
   auto finish = [&](const DownBatch<U>& b, Pos p) {
     const int r0 = p.bb * a.RB, nr = min(a.RB, a.M - r0);
@@ -529,16 +531,18 @@ __global__ __launch_bounds__(WIDE ? 1024 : 640) void k_down_combine(DownArgs a) 
       __syncthreads();
       if (wave == 0 && lane < nr) {
         // weighted_accumulate_f32 over the slots in router order, then the shared experts
-        // with weight 1.0 (engine.rs:5262-5302): o = o + w * d with separate roundings.
+        // with weight 1.0 or their sigmoid gate (engine.rs:5262-5302, :6392-6451):
+        // o = o + w * d with separate roundings.
         float o = 0.0f;
         for (int s = 0; s < a.nslots; s++) {
           float d = 0.0f;
           for (int q = 0; q < a.KS; q++) d += part[s * a.KS + q][lane];
           if (a.round_f16) d = (float)(half_t)d;
-          const float w = s < a.top_k ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), s)) : 1.0f;
+          const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), s));
           o = add_mul_rn(o, w, d);
         }
-        a.out[r0 + lane] = o;
+        // the residual add after the sublayer (engine.rs:5302)
+        a.out[r0 + lane] = a.residual ? a.residual[r0 + lane] + o : o;
       }
       __syncthreads();
     }
@@ -632,6 +636,7 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
                      : a.shared_table + ((size_t)(lane - top_k) * 3 + 2) * a.max_pages;
     my_t = (uint64_t)(uintptr_t)t;
     if (lane < top_k) my_w = a.wts[lane];
+    else if (a.shared_w) my_w = a.shared_w[lane - top_k];  // sigmoid gate of a shared expert
     if (group_pages) {
       typedef __attribute__((address_space(1))) const uint64_t gtab;
       const int r0 = min(R * g0, a.M - 1);
@@ -705,9 +710,7 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
     if (q.p == P - 1) {  // the slot's last pass: its row sums, rounded, into the combine
       float dsum = lanes_sum<L>(acc) * kTwo24;
       if (a.round_f16) dsum = (float)(half_t)dsum;
-      const float w =
-          q.s < top_k ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), q.s))
-                      : 1.0f;
+      const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), q.s));
       const float next = add_mul_rn(o, w, dsum);  // weighted_accumulate_f32 in slot order
       o = keep ? next : o;                         // (engine.rs:5262-5302)
       acc = 0.0f;
@@ -819,7 +822,7 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
   // stored after the loop: a store inside it would share the load counter with the weight
   // loads, and the compiler then waits for all of them at the loop head
   const int r = R * g0 + grp;
-  if (sub == 0 && r < a.M) a.out[r] = o;
+  if (sub == 0 && r < a.M) a.out[r] = a.residual ? a.residual[r] + o : o;  // engine.rs:5302
   VIB3_TRACE_POINT(3);
 }
 

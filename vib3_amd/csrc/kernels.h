@@ -91,6 +91,8 @@ struct DownArgs {
   int RB;
   int round_f16;
   float* out;
+  const float* residual;  // out = residual + sum, or null
+  const float* shared_w;  // [nslots - top_k] weights of the shared experts, or null (1.0)
 };
 
 struct GenericArgs {
@@ -108,6 +110,10 @@ struct GenericArgs {
 int launch_rows(RowsArgs a, bool dual, hipStream_t s, KTime t = {});
 int launch_down(DownArgs a, hipStream_t s, KTime t = {});
 int launch_generic(GenericArgs a, bool dual, hipStream_t s);
+// RMSNorm of x into xn (norm_w set) and the shared experts' sigmoid gates (gate_w set).
+int launch_moe_prologue(const void* x, int x_dt, const uint16_t* norm_w, float eps, int D,
+                        float* xn, const uint16_t* gate_w, int ns, float* shared_w,
+                        hipStream_t st);
 
 constexpr int kMaxExperts = 4096;
 

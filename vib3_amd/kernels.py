@@ -131,6 +131,48 @@ def weighted_accumulate_f32(output: torch.Tensor, expert_output: torch.Tensor, w
               dim, _stream(output))
 
 
+def rms_norm_f32(input: torch.Tensor, output: torch.Tensor, weight: torch.Tensor, dim: int,
+                 eps: float) -> None:
+    """kernels.rs:1567 rms_norm_f32: output = input * inv_rms * weight (f32 in/out, f16 weight);
+    output f16 gives kernels.rs:1604 rms_norm_f32_to_f16."""
+    if input.dtype != torch.float32 or weight.dtype != torch.float16:
+        raise TypeError("rms_norm_f32 takes an f32 input and f16 weights")
+    if output.dtype == torch.float32:
+        name = "vib3_launch_rms_norm_f32"
+    elif output.dtype == torch.float16:
+        name = "vib3_launch_rms_norm_f32_to_f16"
+    else:
+        raise TypeError("output must be f32 or f16")
+    _lib.call(name, _dev(input, "input"), _dev(output, "output"), _dev(weight, "weight"), dim,
+              float(eps), _stream(input))
+
+
+def rms_norm_f32_to_f16(input, output, weight, dim, eps) -> None:
+    """kernels.rs:1604."""
+    if output.dtype != torch.float16:
+        raise TypeError("output must be f16")
+    rms_norm_f32(input, output, weight, dim, eps)
+
+
+def residual_add_f32_f32(accumulator: torch.Tensor, layer_output: torch.Tensor, dim: int) -> None:
+    """kernels.rs:2195: accumulator += layer_output (both f32)."""
+    if accumulator.dtype != torch.float32 or layer_output.dtype != torch.float32:
+        raise TypeError("residual_add_f32_f32 takes f32 tensors")
+    _lib.call("vib3_launch_residual_add_f32_f32", _dev(accumulator, "accumulator"),
+              _dev(layer_output, "layer_output"), dim, _stream(accumulator))
+
+
+def sigmoid_gated_accumulate_f32(output: torch.Tensor, expert_output: torch.Tensor,
+                                 gate_dev: torch.Tensor, dim: int) -> None:
+    """kernels.rs:2080: output += sigmoid(gate_dev[0]) * expert_output (f16)."""
+    if output.dtype != torch.float32 or expert_output.dtype != torch.float16 or \
+            gate_dev.dtype != torch.float32:
+        raise TypeError("sigmoid_gated_accumulate_f32 takes f32 output/gate and f16 expert output")
+    _lib.call("vib3_launch_sigmoid_gated_accumulate_f32", _dev(output, "output"),
+              _dev(expert_output, "expert_output"), _dev(gate_dev, "gate_dev"), dim,
+              _stream(output))
+
+
 def _scoring(scoring_func) -> Tuple[int, float, int]:
     if isinstance(scoring_func, Sigmoid):
         return ROUTER_SIGMOID, float(scoring_func.scaling_factor), int(scoring_func.normalize)

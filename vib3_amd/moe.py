@@ -147,8 +147,14 @@ class MoeInt4Layer:
 
     def __init__(self, bank: Int4ExpertBank, router_w: Optional[torch.Tensor],
                  router_bias: Optional[torch.Tensor], top_k: int, scoring_mode: int,
-                 scaling_factor: float = 1.0, normalize: bool = True, flags: int = 0):
+                 scaling_factor: float = 1.0, normalize: bool = True, flags: int = 0,
+                 norm_weight: Optional[torch.Tensor] = None, norm_eps: float = 1e-6,
+                 shared_gate: Optional[torch.Tensor] = None):
+        """norm_weight (f16 [hidden]): launch() takes the f32 residual stream and normalises it
+        inside the layer; shared_gate (f16 [num_shared][hidden]): sigmoid-gated shared
+        experts. launch(..., residual=r) returns r + sublayer."""
         self.bank, self.router_w, self.router_bias = bank, router_w, router_bias
+        self.norm_weight, self.norm_eps, self.shared_gate = norm_weight, norm_eps, shared_gate
         self.top_k, self.scoring_mode = top_k, scoring_mode
         self.scaling_factor, self.normalize, self.flags = scaling_factor, normalize, flags
         dev = bank.device
@@ -187,16 +193,26 @@ class MoeInt4Layer:
         d.out_ids = self.ids.data_ptr()
         d.out_weights = self.wts.data_ptr()
         d.out_scores = self.scores.data_ptr()
+        if self.norm_weight is not None:
+            d.norm_weight = self.norm_weight.data_ptr()
+            d.norm_eps = self.norm_eps
+        if self.shared_gate is not None:
+            d.shared_gate = self.shared_gate.data_ptr()
         if hasattr(self, "workspace"):
             d.workspace = self.workspace.data_ptr()
             d.workspace_bytes = self.workspace.numel()
         return d
 
     def launch(self, x: torch.Tensor, in_ids: Optional[torch.Tensor] = None,
-               in_wts: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+               in_wts: Optional[torch.Tensor] = None, stream=None,
+               residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         if not x.is_cuda or not x.is_contiguous():
             raise TypeError("x must be a contiguous device tensor")
         desc = self._desc(x, in_ids, in_wts)
+        if residual is not None:
+            if residual.dtype != torch.float32 or residual.numel() != self.bank.shape.hidden:
+                raise TypeError("residual must be f32 [hidden]")
+            desc.residual = residual.data_ptr()
         st = (stream or torch.cuda.current_stream(x.device)).cuda_stream
         rc = _lib.load().vib3_launch_moe_int4_layer(desc, st)
         if rc != 0:
