@@ -229,6 +229,9 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--sublayer", action="store_true",
+                    help="the whole MoE sublayer as the engine runs it: x is the f32 residual "
+                         "stream, RMSNorm + shared-expert sigmoid gate + residual add fused in")
     ap.add_argument("--given-ids", action="store_true",
                     help="skip the router: experts come from preset device id lists (diagnostic)")
     args = ap.parse_args()
@@ -267,12 +270,24 @@ def main() -> int:
                                   device=dev)
         w, b = moe.make_router(shape, l, cfg["seed"], cfg["router_sigma"], cfg["bias_sigma"],
                                device=dev)
+        extra = {}
+        if args.sublayer:
+            g = torch.Generator(device="cpu").manual_seed(cfg["seed"] + l)
+            extra = dict(
+                norm_weight=(1 + 0.1 * torch.randn(cfg["hidden"], generator=g)).half().to(dev),
+                norm_eps=1e-6,
+                shared_gate=(0.02 * torch.randn(cfg["shared"], cfg["hidden"], generator=g))
+                .half().to(dev) if cfg["shared"] else None)
         layers.append(moe.MoeInt4Layer(bank, w, b, top_k=cfg["k"], scoring_mode=cfg["mode"],
-                                       scaling_factor=cfg["scaling"], normalize=True))
+                                       scaling_factor=cfg["scaling"], normalize=True, **extra))
         torch.cuda.synchronize()
         log(f"[bench] layer {l} ready ({bank.nbytes / 1e9:.2f} GB, {time.perf_counter() - t0:.1f}s)")
+    if args.sublayer:  # the residual stream between decoder layers: f32, large magnitudes
+        tdt = torch.float32
     xs = [moe.make_activation(cfg["hidden"], t, cfg["seed"], dtype=tdt, device=dev)
           for t in range(args.tokens)]
+    if args.sublayer:
+        xs = [x * 20.0 for x in xs]
     if args.given_ids:
         rng = np.random.default_rng(cfg["seed"])
         gid = [torch.from_numpy(rng.choice(cfg["E"], cfg["k"], replace=False).astype(np.int16)).to(dev)
@@ -283,6 +298,10 @@ def main() -> int:
         descs = [[ly._desc(x, gid[t], gw) for t, x in enumerate(xs)] for ly in layers]
     else:
         descs = [[ly._desc(x) for x in xs] for ly in layers]
+    if args.sublayer:  # out = x + MoE(RMSNorm(x)), engine.rs:5064-5307
+        for row in descs:
+            for d, x in zip(row, xs):
+                d.residual = x.data_ptr()
     lib = _lib.load()
     launch = lib.vib3_launch_moe_int4_layer
     L = len(layers)
@@ -312,7 +331,9 @@ def main() -> int:
     fused = bool(lib.vib3_moe_int4_router_fused(descs[0][0]))
     stage_us = {}
     for j, name in enumerate(("router", "gateup", "down")):
-        if name == "router" and (args.given_ids or fused):
+        if name == "router" and args.sublayer and fused:
+            name = "prologue"  # RMSNorm + shared gates; the router is inside gate/up
+        elif name == "router" and (args.given_ids or fused):
             continue  # no router launches: the gate/up kernel computes the logits itself
         s0, s1 = _hip.Event(), _hip.Event()
         s0.record(st)
@@ -357,7 +378,7 @@ def main() -> int:
             traffic = json.load(f)["kernels"].get("k_int4_rows", {}).get("hbm_bytes")
 
     cpu = None
-    if not args.no_cpu and not args.given_ids:
+    if not args.no_cpu and not args.given_ids and not args.sublayer:
         ly = layers[0]
         x = xs[0]
         ly.launch(x)
@@ -382,7 +403,10 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int4 weights x bf16 activations, f32 accumulate",
         "data": "synthetic (counter-based generator; random-init weights of the named shape)",
-        "config": {"workload": cfg["workload"], "layers_rotated": L, "tokens": args.tokens,
+        "config": {"workload": cfg["workload"] + ("; whole sublayer: f32 residual stream in, "
+                                                  "RMSNorm, sigmoid-gated shared expert, "
+                                                  "residual add" if args.sublayer else ""),
+                   "layers_rotated": L, "tokens": args.tokens,
                    "layout": cfg["layout"], "algorithmic_bytes_per_layer": nbytes["layer"]},
         "roofline": {"bound": "hbm",
                      "kernel": "k_int4_rows<4,true> (router logits + top-k + gate/up GEMV + SwiGLU)"

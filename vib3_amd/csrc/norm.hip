@@ -16,13 +16,22 @@
 namespace vib3 {
 
 // Inverse RMS of x[0..D) for a 256-thread workgroup, in the reference's summation order.
+// Up to 8192 elements every load is issued before the first add (one round trip).
 __device__ float wg_inv_rms(const float* x, int D, float eps) {
   __shared__ float ss[256];
   const int tid = (int)threadIdx.x;
   float p = 0.0f;
-  for (int d = tid; d < D; d += 256) {
-    const float v = x[d];
-    p = __builtin_fmaf(v, v, p);
+  if (D <= 256 * 32) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) v[i] = tid + 256 * i < D ? x[tid + 256 * i] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) p = __builtin_fmaf(v[i], v[i], p);
+  } else {
+    for (int d = tid; d < D; d += 256) {
+      const float v = x[d];
+      p = __builtin_fmaf(v, v, p);
+    }
   }
   ss[tid] = p;
   __syncthreads();
@@ -36,9 +45,13 @@ __device__ float wg_inv_rms(const float* x, int D, float eps) {
   return inv;
 }
 
-__device__ __forceinline__ float norm_elem(float x, float inv, uint16_t w) {
+__device__ __forceinline__ float norm_mul(float x, float inv, float w) {
 #pragma clang fp contract(off)
-  return x * inv * f16_to_f32(w);
+  return x * inv * w;
+}
+
+__device__ __forceinline__ float norm_elem(float x, float inv, uint16_t w) {
+  return norm_mul(x, inv, f16_to_f32(w));
 }
 
 // RMSNorm of an f32 vector with f16 weights; OUT_F16 rounds the result to f16. Workgroup b
@@ -76,6 +89,11 @@ __global__ void k_sigmoid_gated_acc(float* out, const uint16_t* e, const float* 
 // xn = RMSNorm(x) (f32, as engine.rs's moe_normed_f32) when a norm weight is given;
 // workgroup nblk + s computes shared expert s's gate logit  g = xn . f32(gate_w[s]) and stores
 // sigmoid(g) = 1 / (1 + exp(-g)), the weight of that expert's output (engine.rs:6392-6425).
+// Thread t holds elements t + 256 i (i < kProMax, D <= 256 * kProMax): the layout of the
+// reference's partial sums, so every load of a workgroup is issued at once (one round trip)
+// and the normalised values it writes are already in its registers.
+constexpr int kProMax = 32;
+
 struct PrologueArgs {
   const void* x;
   int x_dt;
@@ -89,40 +107,88 @@ struct PrologueArgs {
   float* shared_w;         // [ns]
 };
 
+template <int XDT>
 __global__ __launch_bounds__(256) void k_moe_prologue(PrologueArgs a) {
   const int b = (int)blockIdx.x, tid = (int)threadIdx.x;
-  const float inv = a.norm_w ? wg_inv_rms((const float*)a.x, a.D, a.eps) : 1.0f;
-  auto xn_at = [&](int d) {
-    return a.norm_w ? norm_elem(((const float*)a.x)[d], inv, a.norm_w[d])
-                    : load_act(a.x, a.x_dt, (size_t)d);
-  };
-  if (b < a.nblk) {
-    const int d0 = b * 1024;
-    for (int d = d0 + tid; d < min(a.D, d0 + 1024); d += 256) a.xn[d] = xn_at(d);
+  const bool gate = b >= a.nblk;
+  const int D = a.D;
+  float xv[kProMax], wv[kProMax], gv[kProMax];
+  // raw loads first, all unconditional (indices past D clamp to 0 and are zeroed after), so
+  // the whole workgroup's data is one round trip
+  uint32_t xr[kProMax];
+  uint16_t wr[kProMax], gr[kProMax];
+  const uint16_t* nw = a.norm_w ? a.norm_w : (const uint16_t*)a.x;
+  const uint16_t* gw = gate ? a.gate_w + (size_t)(b - a.nblk) * D : (const uint16_t*)a.x;
+#pragma unroll
+  for (int i = 0; i < kProMax; i++) {
+    const int d = tid + 256 * i < D ? tid + 256 * i : 0;
+    xr[i] = XDT == VIB3_DT_F32 ? ((const uint32_t*)a.x)[d] : ((const uint16_t*)a.x)[d];
+    wr[i] = nw[d];
+    gr[i] = gw[d];
+  }
+#pragma unroll
+  for (int i = 0; i < kProMax; i++) {
+    const bool in = tid + 256 * i < D;
+    const float xf = XDT == VIB3_DT_F32   ? __uint_as_float(xr[i])
+                     : XDT == VIB3_DT_F16 ? f16_to_f32((uint16_t)xr[i])
+                                          : bf16_to_f32((uint16_t)xr[i]);
+    xv[i] = in ? xf : 0.0f;
+    wv[i] = a.norm_w ? f16_to_f32(wr[i]) : 1.0f;
+    gv[i] = in && gate ? f16_to_f32(gr[i]) : 0.0f;
+  }
+  float inv = 1.0f;
+  if (a.norm_w) {
+    __shared__ float ss[256];
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kProMax; i++) p = __builtin_fmaf(xv[i], xv[i], p);  // zeros past D
+    ss[tid] = p;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+      if (tid < s) ss[tid] += ss[tid + s];
+      __syncthreads();
+    }
+    const float rms = sqrtf(ss[0] / (float)D + a.eps);
+    inv = 1.0f / rms;
+#pragma unroll
+    for (int i = 0; i < kProMax; i++) xv[i] = norm_mul(xv[i], inv, wv[i]);
+  }
+  if (!gate) {
+    // this workgroup's 1024 elements: i = 4b .. 4b + 3
+#pragma unroll
+    for (int i = 0; i < kProMax; i++) {
+      const int d = tid + 256 * i;
+      if (i / 4 == b && d < D) a.xn[d] = xv[i];
+    }
     return;
   }
-  const int s = b - a.nblk;
-  const uint16_t* gw = a.gate_w + (size_t)s * a.D;
   float acc = 0.0f;
-  for (int d = tid; d < a.D; d += 256) acc = __builtin_fmaf(xn_at(d), f16_to_f32(gw[d]), acc);
+#pragma unroll
+  for (int i = 0; i < kProMax; i++) acc = __builtin_fmaf(xv[i], gv[i], acc);
   __shared__ float red[4];
   acc = wave_sum(acc);
   if ((tid & 63) == 0) red[tid >> 6] = acc;
   __syncthreads();
   if (tid == 0) {
     const float g = (red[0] + red[1]) + (red[2] + red[3]);
-    a.shared_w[s] = 1.0f / (1.0f + expf(-g));
+    a.shared_w[b - a.nblk] = 1.0f / (1.0f + expf(-g));
   }
 }
 
 int launch_moe_prologue(const void* x, int x_dt, const uint16_t* norm_w, float eps, int D,
                         float* xn, const uint16_t* gate_w, int ns, float* shared_w,
                         hipStream_t st) {
+  if (D > 256 * kProMax) return VIB3_ERR_UNSUPPORTED;
   PrologueArgs a{x, x_dt, norm_w, eps, D, xn, norm_w ? (D + 1023) / 1024 : 0, gate_w,
                  gate_w ? ns : 0, shared_w};
   const int grid = a.nblk + a.ns;
   if (grid == 0) return 0;
-  hipLaunchKernelGGL(k_moe_prologue, dim3((unsigned)grid), dim3(256), 0, st, a);
+  if (x_dt == VIB3_DT_F32)
+    hipLaunchKernelGGL(k_moe_prologue<VIB3_DT_F32>, dim3((unsigned)grid), dim3(256), 0, st, a);
+  else if (x_dt == VIB3_DT_F16)
+    hipLaunchKernelGGL(k_moe_prologue<VIB3_DT_F16>, dim3((unsigned)grid), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(k_moe_prologue<VIB3_DT_BF16>, dim3((unsigned)grid), dim3(256), 0, st, a);
   VIB3_RETURN_LAUNCH();
 }
 
