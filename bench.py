@@ -206,7 +206,7 @@ def bench_c4(args, cfg) -> int:
         "config": {"workload": cfg["workload"], "layers_rotated": L, "batches": nb,
                    "distinct_experts_per_batch": round(float(np.mean(distinct)), 1),
                    "algorithmic_bytes_per_batch": round(avg_bytes)},
-        "roofline": {"bound": "hbm", "kernel": "k_mx_gemm (gate/up + down grouped GEMM, whole batch)",
+        "roofline": {"bound": "hbm", "kernel": "k_mx_rows + k_mx_gemm (row path and matrix-core grouped GEMM, gate/up + down, whole batch)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": "profiles/traffic_c4.json" if traffic else None},
@@ -375,7 +375,9 @@ def main() -> int:
     tpath = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
     if os.path.exists(tpath) and not args.given_ids:
         with open(tpath) as f:
-            traffic = json.load(f)["kernels"].get("k_int4_rows", {}).get("hbm_bytes")
+            kern = json.load(f)["kernels"]
+            traffic = next((v["hbm_bytes"] for k, v in kern.items()
+                            if k.startswith("k_int4_rows")), None)
 
     cpu = None
     if not args.no_cpu and not args.given_ids and not args.sublayer:

@@ -2,6 +2,11 @@
 
     python -m vib3_amd.profile_summary trace <db>   per-kernel dispatch count and durations
     python -m vib3_amd.profile_summary pmc <db>     per-kernel average of each PMC counter
+    python -m vib3_amd.profile_summary traffic <fetch_db> <write_db> <out.json> <source>
+                                               [<cal_fetch_db> <cal_write_db>]
+        HBM bytes per dispatch of each kernel: FETCH_SIZE and WRITE_SIZE (KiB) scaled by what
+        the same counter reads for the bench's 1 GiB device copies (the calibration; taken from
+        the optional databases when the runs themselves hold no copy, as bench --config c4)
 
 Only kernels of this library and the runtime copy kernels are listed (the synthetic-weight
 generator kernels are skipped).
@@ -48,8 +53,61 @@ def pmc(db: str) -> None:
               f"(avg {d / 1000:.1f} us)")
 
 
+def _kernel_key(name: str) -> str:
+    """`void vib3::k_mx_gemm<true, 4>(vib3::MxArgs)` -> `k_mx_gemm<true, 4>`."""
+    short = name.split("vib3::", 1)[-1]
+    depth = 0
+    for i, ch in enumerate(short):
+        depth += ch == "<"
+        depth -= ch == ">"
+        if ch == "(" and depth == 0:
+            return short[:i]
+    return short
+
+
+def _counter(db: str, counter: str):
+    con = sqlite3.connect(db)
+    per = {}
+    for k, v in con.execute("select kernel_name, avg(value) from counters_collection "
+                            "where counter_name = ? group by kernel_name", (counter,)):
+        if "vib3::" in k and "synth" not in k:
+            per[_kernel_key(k)] = float(v)
+    cal = con.execute("select avg(value) from counters_collection where counter_name = ? and "
+                      "kernel_name like '%copy%' and duration > 200000", (counter,)).fetchone()[0]
+    return per, cal
+
+
+def traffic(fetch_db: str, write_db: str, out: str, source: str, cal_fetch_db: str = "",
+            cal_write_db: str = "") -> None:
+    import json
+    fetch, fcal = _counter(fetch_db, "FETCH_SIZE")
+    write, wcal = _counter(write_db, "WRITE_SIZE")
+    if fcal is None and cal_fetch_db:
+        fcal = _counter(cal_fetch_db, "FETCH_SIZE")[1]
+    if wcal is None and cal_write_db:
+        wcal = _counter(cal_write_db, "WRITE_SIZE")[1]
+    gib_kib = float(1 << 20)
+    ff, wf = gib_kib / fcal, gib_kib / wcal  # counter KiB -> bytes moved, per the copy kernels
+    res = {"source": source,
+           "calibration": {"copy_bytes_each_way": 1 << 30, "FETCH_SIZE_KiB": round(fcal, 1),
+                           "WRITE_SIZE_KiB": round(wcal, 1), "fetch_factor": round(ff, 4),
+                           "write_factor": round(wf, 4)},
+           "kernels": {}}
+    for k in sorted(set(fetch) | set(write)):
+        f, w = fetch.get(k, 0.0), write.get(k, 0.0)
+        res["kernels"][k] = {"FETCH_SIZE_KiB": round(f, 1), "WRITE_SIZE_KiB": round(w, 1),
+                             "hbm_bytes": round((f * ff + w * wf) * 1024)}
+    with open(out, "w") as fh:
+        json.dump(res, fh, indent=1)
+        fh.write("\n")
+    print(json.dumps(res, indent=1))
+
+
 if __name__ == "__main__":
-    if len(sys.argv) != 3 or sys.argv[1] not in ("trace", "pmc"):
+    if len(sys.argv) in (6, 8) and sys.argv[1] == "traffic":
+        traffic(*sys.argv[2:])
+    elif len(sys.argv) == 3 and sys.argv[1] in ("trace", "pmc"):
+        (trace if sys.argv[1] == "trace" else pmc)(sys.argv[2])
+    else:
         print(__doc__, file=sys.stderr)
         sys.exit(2)
-    (trace if sys.argv[1] == "trace" else pmc)(sys.argv[2])
