@@ -43,6 +43,8 @@ extern "C" {
 #define VIB3_ERR_BAD_COUNT (-2)
 #define VIB3_ERR_BAD_POINTER (-3)
 #define VIB3_ERR_WORKSPACE (-4)
+#define VIB3_ERR_FORMAT (-5) /* a .vib3 file or its page layout is not what the reader expects */
+#define VIB3_ERR_IO (-6)     /* a .vib3 file could not be opened or mapped */
 
 /* ------------------------------------------------------------------------------------------
  * Reference-compatible launchers: same names, argument order and meaning as cuda_ffi.rs.
@@ -242,6 +244,62 @@ typedef struct vib3_moe_mxfp4_batch {
 
 size_t vib3_moe_mxfp4_workspace_bytes(const vib3_moe_mxfp4_batch *batch);
 int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch *batch, void *stream);
+
+/* ------------------------------------------------------------------------------------------
+ * The .vib3 model file (host side; format.rs). The file is memory-mapped read-only; page data
+ * is returned as host pointers into the mapping, for the caller to upload where its page pool
+ * lives. vib3_build_page_table then writes the fused layer's page table from the catalog.
+ * ---------------------------------------------------------------------------------------- */
+
+typedef struct vib3_file vib3_file; /* opaque: the mapping plus the parsed catalog */
+
+/* Header summary (format.rs:50-92 Vib3Header). expert_dtype / shared_dtype use the reference's
+ * DType codes (types.rs:633: 0 FP16, 1 BF16, 5 INT4, 7 NVFP4, ...). */
+typedef struct vib3_file_info {
+    uint32_t num_layers, num_experts, num_active_experts, hidden_dim, expert_hidden_dim;
+    uint8_t expert_dtype, shared_dtype;
+    uint32_t page_count;
+    uint64_t page_data_offset, page_data_size;
+} vib3_file_info;
+
+/* One page catalog entry (format.rs:101-125 PageCatalogEntry) and its index in the catalog. */
+typedef struct vib3_page_entry {
+    uint16_t layer, expert, segment, page_idx; /* types.rs:201 PageId */
+    uint64_t file_offset;
+    uint32_t compressed_size, raw_size;
+    uint16_t row_start, row_count, col_start, col_count;
+    uint8_t compression, flags; /* compression: 0 none, 1 LZ4, 2 zstd (format.rs:43-45) */
+    uint32_t catalog_index;
+} vib3_page_entry;
+
+/* format.rs:241 Vib3File::open: magic/version checked, catalog and expert index parsed. */
+int vib3_file_open(const char *path, vib3_file **out);
+void vib3_file_close(vib3_file *file);
+int vib3_file_get_info(const vib3_file *file, vib3_file_info *info);
+/* The model metadata section (JSON, format.rs:263-272), not NUL-terminated. */
+int vib3_file_metadata(const vib3_file *file, const char **json, size_t *len);
+/* Catalog entry `index` (format.rs:355). */
+int vib3_file_page(const vib3_file *file, uint32_t index, vib3_page_entry *entry);
+/* format.rs:371 pages_for_expert: the entries of (layer, expert) in catalog order (segment,
+ * then page_idx); *count = their number (at most max_entries are written). expert 0xFFFF is
+ * the layer's shared tensors (router segment 3, norms, shared experts 14/15/16, gate 26). */
+int vib3_file_expert_pages(const vib3_file *file, uint16_t layer, uint16_t expert,
+                           vib3_page_entry *out, int max_entries, int *count);
+/* format.rs:501 read_page_sync for an uncompressed page: a pointer into the mapping and its
+ * size. Compressed pages return VIB3_ERR_UNSUPPORTED (no LZ4/zstd codec in this build). */
+int vib3_file_page_data(const vib3_file *file, uint32_t index, const void **data, size_t *size);
+
+/* The page table of vib3_moe_int4_layer from the catalog (engine.rs:1236-1299, one page per
+ * segment there; any number here): for each experts[i] of `layer` and each of its segments
+ * segments[0..2] (up, gate, down: {0, 1, 2} for routed experts, {14, 15, 16} for shared ones),
+ * table[(i*3 + s)*max_pages + page_idx] = page_addr[catalog index of that page] (where the
+ * caller put the page, 0 = not resident, which is an error). rows_per_page[s] receives the
+ * segment's rows per page; pages must cover rows [p*rows_per_page, ...) in order (the
+ * converter's layout, convert.rs:1852-1865). Host memory in, host memory out. */
+int vib3_build_page_table(const vib3_file *file, uint16_t layer, const uint16_t *experts,
+                          int num_experts, const uint16_t segments[3],
+                          const uint64_t *page_addr, uint64_t *table, int max_pages,
+                          int rows_per_page[3]);
 
 /* ------------------------------------------------------------------------------------------
  * Utilities

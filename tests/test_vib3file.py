@@ -1,0 +1,103 @@
+"""The .vib3 reader (vib3_file_*) and the page-table builder on the CPU: header, metadata,
+catalog order, page bytes, the table of every expert's segments, and the error paths. The
+files come from tests/vib3_writer.py, which follows the reference writer's layout
+(format.rs:842-1030). No GPU call."""
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from vib3_writer import make_test_model
+
+
+@pytest.fixture(scope="module")
+def model(tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("vib3") / "model.vib3")
+    cfg, dense = make_test_model(path)
+    return path, cfg, dense
+
+
+def test_header_metadata_and_catalog(model):
+    from vib3_amd.vib3file import Vib3File
+    path, cfg, dense = model
+    with Vib3File(path) as f:
+        i = f.info
+        assert (i.num_layers, i.num_experts, i.num_active_experts, i.hidden_dim,
+                i.expert_hidden_dim, i.expert_dtype, i.shared_dtype) == (1, 8, 2, 1024, 256, 5, 0)
+        assert i.page_count == len(dense["pages"])
+        assert i.page_data_offset % (2 << 20) == 0
+        assert f.metadata["scoring_func"] == "sigmoid"
+        assert f.metadata["routed_scaling_factor"] == pytest.approx(2.827)
+        # catalog sorted by (layer, expert, segment, page_idx); expert 3 has 3 + 3 + 3 pages
+        e3 = f.expert_pages(0, 3)
+        assert [(p.segment, p.page_idx) for p in e3] == [(s, q) for s in range(3) for q in range(3)]
+        assert [p.row_start for p in e3[:3]] == [0, 96, 192]
+        assert [p.row_count for p in e3[6:]] == [400, 400, 224]
+        want = {(p[0], p[1], p[2], p[3]): p[7] for p in dense["pages"]}
+        for p in e3 + f.expert_pages(0, 0xFFFF):
+            assert f.page_bytes(p.catalog_index).tobytes() == want[(p.layer, p.expert,
+                                                                     p.segment, p.page_idx)]
+            assert p.file_offset % 4096 == 0
+        router = f.segment_bytes(0, 0xFFFF, 3).view(np.uint16)
+        assert np.array_equal(router, dense["router"])
+        assert f.expert_pages(0, 100) == []
+
+
+def test_page_table(model):
+    from vib3_amd.vib3file import Vib3File
+    path, _, _ = model
+    with Vib3File(path) as f:
+        addr = np.arange(f.info.page_count, dtype=np.uint64) * 4096 + (1 << 40)
+        table, rpp = f.build_page_table(0, list(range(8)), (0, 1, 2), addr, 3)
+        assert rpp == [96, 96, 400]
+        table = table.reshape(8, 3, 3)
+        for e in range(8):
+            for p in f.expert_pages(0, e):
+                assert table[e, p.segment, p.page_idx] == addr[p.catalog_index]
+        shared, srpp = f.build_page_table(0, [0xFFFF], (14, 15, 16), addr, 3)
+        assert srpp == [96, 96, 400] and np.all(shared != 0)
+        # a page that is not resident (address 0) is an error, as is a missing expert
+        gap = addr.copy()
+        gap[f.expert_pages(0, 5)[1].catalog_index] = 0
+        with pytest.raises(Exception) as err:
+            f.build_page_table(0, list(range(8)), (0, 1, 2), gap, 3)
+        assert getattr(err.value, "code", None) == -5
+        with pytest.raises(Exception):
+            f.build_page_table(0, [9], (0, 1, 2), addr, 3)
+        with pytest.raises(Exception):  # max_pages too small for the 3 pages of a segment
+            f.build_page_table(0, [0], (0, 1, 2), addr, 2)
+
+
+def test_errors(model, tmp_path):
+    from vib3_amd._lib import Vib3Error
+    from vib3_amd.vib3file import Vib3File
+    path, _, _ = model
+    with pytest.raises(Vib3Error) as e:
+        Vib3File(str(tmp_path / "missing.vib3"))
+    assert e.value.code == -6
+    bad = tmp_path / "bad.vib3"
+    raw = bytearray(open(path, "rb").read(4096))
+    raw[0:8] = struct.pack("<Q", 0x1234)
+    bad.write_bytes(bytes(raw))
+    with pytest.raises(Vib3Error) as e:
+        Vib3File(str(bad))
+    assert e.value.code == -5
+    trunc = tmp_path / "trunc.vib3"
+    trunc.write_bytes(open(path, "rb").read(600))  # the catalog runs past the end
+    with pytest.raises(Vib3Error) as e:
+        Vib3File(str(trunc))
+    assert e.value.code == -5
+
+
+def test_compressed_pages_are_refused(tmp_path):
+    from vib3_amd._lib import Vib3Error
+    from vib3_amd.vib3file import Vib3File
+    path = str(tmp_path / "lz4.vib3")
+    make_test_model(path, E=2, compressed={(0, 1, 2, 0)})
+    with Vib3File(path) as f:
+        p = [q for q in f.expert_pages(0, 1) if q.segment == 2][0]
+        assert p.compression == 1
+        with pytest.raises(Vib3Error) as e:
+            f.page_bytes(p.catalog_index)
+        assert e.value.code == -1

@@ -18,7 +18,8 @@ ROUTER_SOFTMAX, ROUTER_SIGMOID = 0, 1
 MOE_F32_INTERMEDIATE = 1
 
 ERRORS = {-1: "unsupported shape or dtype", -2: "bad count", -3: "bad pointer or alignment",
-          -4: "workspace too small"}
+          -4: "workspace too small", -5: "unexpected .vib3 file or page layout",
+          -6: ".vib3 file cannot be opened"}
 
 
 class Vib3Error(RuntimeError):
@@ -89,6 +90,14 @@ SIGNATURES = {
     "vib3_synth_normal": (I, [P, I, S, U64, U64, S, F, P]),
     "vib3_synth_int4_page": (I, [P, U64, U64, I, I, I, F, I, I, P]),
     "vib3_synth_mxfp4_page": (I, [P, U64, U64, I, I, I, P]),
+    "vib3_file_open": (I, [C.c_char_p, P]),
+    "vib3_file_close": (None, [P]),
+    "vib3_file_get_info": (I, [P, P]),
+    "vib3_file_metadata": (I, [P, P, P]),
+    "vib3_file_page": (I, [P, C.c_uint32, P]),
+    "vib3_file_expert_pages": (I, [P, C.c_uint16, C.c_uint16, P, I, P]),
+    "vib3_file_page_data": (I, [P, C.c_uint32, P, P]),
+    "vib3_build_page_table": (I, [P, C.c_uint16, P, I, P, P, P, I, P]),
     "vib3_hip_version": (C.c_char_p, []),
 }
 

@@ -8,7 +8,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libvib3_hip.so")
-SOURCES = ["api.hip", "int4_gemv.hip", "router.hip", "synth.hip", "mxfp4_moe.hip", "norm.hip"]
+SOURCES = ["api.hip", "int4_gemv.hip", "router.hip", "synth.hip", "mxfp4_moe.hip", "norm.hip",
+           "vib3file.cpp"]
 ARCH = os.environ.get("VIB3_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

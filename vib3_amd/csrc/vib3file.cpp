@@ -1,0 +1,244 @@
+// vib3file.cpp — host-side reader of the reference's `.vib3` model file (format.rs) and the
+// builder of the fused layer's page table from it (engine.rs:1236-1299, generalised to several
+// pages per segment). Host code only: the file is memory-mapped read-only, nothing touches the
+// GPU, and the caller uploads pages and the table wherever it keeps them.
+//
+// On-disk layout (format.rs:9-26, :48-140; all structures little-endian and packed):
+//   header (512 B) | model metadata (JSON) | page catalog (48 B entries, sorted by
+//   (layer, expert, segment, page_idx)) | expert index (20 B entries) | ... | page data (2 MiB
+//   aligned section, each page 4 KiB aligned).
+#include <errno.h>
+#include <fcntl.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <new>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/vib3_hip.h"
+
+namespace {
+
+constexpr uint64_t kMagic = 0x3342495600000001ull;  // format.rs:39 VIB3_MAGIC
+constexpr uint32_t kVersion = 1;
+constexpr size_t kHeaderSize = 512;
+constexpr size_t kCatalogEntry = 48;
+constexpr size_t kExpertEntry = 20;
+
+template <typename T>
+T rd(const uint8_t* p) {
+  T v;
+  memcpy(&v, p, sizeof(T));
+  return v;
+}
+
+struct ExpertRange {
+  uint32_t first, count;
+};
+
+}  // namespace
+
+struct vib3_file {
+  int fd = -1;
+  const uint8_t* map = nullptr;
+  size_t size = 0;
+  vib3_file_info info{};
+  const uint8_t* metadata = nullptr;
+  size_t metadata_size = 0;
+  std::vector<vib3_page_entry> catalog;
+  std::unordered_map<uint32_t, ExpertRange> experts;  // layer << 16 | expert
+};
+
+namespace {
+
+// Header fields at their packed offsets (format.rs:50-92).
+int parse(vib3_file* f) {
+  const uint8_t* h = f->map;
+  if (f->size < kHeaderSize) return VIB3_ERR_FORMAT;
+  if (rd<uint64_t>(h + 0) != kMagic || rd<uint32_t>(h + 8) != kVersion) return VIB3_ERR_FORMAT;
+  const uint64_t meta_off = rd<uint64_t>(h + 16), meta_size = rd<uint64_t>(h + 24);
+  const uint64_t cat_off = rd<uint64_t>(h + 32);
+  const uint32_t cat_count = rd<uint32_t>(h + 48);
+  const uint64_t ei_off = rd<uint64_t>(h + 52), ei_size = rd<uint64_t>(h + 60);
+  vib3_file_info& in = f->info;
+  in.page_data_offset = rd<uint64_t>(h + 120);
+  in.page_data_size = rd<uint64_t>(h + 128);
+  in.num_layers = rd<uint32_t>(h + 136);
+  in.num_experts = rd<uint32_t>(h + 140);
+  in.num_active_experts = rd<uint32_t>(h + 144);
+  in.hidden_dim = rd<uint32_t>(h + 148);
+  in.expert_hidden_dim = rd<uint32_t>(h + 152);
+  in.expert_dtype = h[156];
+  in.shared_dtype = h[157];
+  in.page_count = cat_count;
+  if (meta_off > f->size || meta_size > f->size - meta_off) return VIB3_ERR_FORMAT;
+  f->metadata = h + meta_off;
+  f->metadata_size = (size_t)meta_size;
+  if (cat_off > f->size || (uint64_t)cat_count * kCatalogEntry > f->size - cat_off)
+    return VIB3_ERR_FORMAT;
+  f->catalog.resize(cat_count);
+  for (uint32_t i = 0; i < cat_count; i++) {
+    const uint8_t* e = h + cat_off + (size_t)i * kCatalogEntry;  // format.rs:101-125
+    vib3_page_entry& p = f->catalog[i];
+    p.layer = rd<uint16_t>(e + 0);
+    p.expert = rd<uint16_t>(e + 2);
+    p.segment = rd<uint16_t>(e + 4);
+    p.page_idx = rd<uint16_t>(e + 6);
+    p.file_offset = rd<uint64_t>(e + 8);
+    p.compressed_size = rd<uint32_t>(e + 16);
+    p.raw_size = rd<uint32_t>(e + 20);
+    p.row_start = rd<uint16_t>(e + 24);
+    p.row_count = rd<uint16_t>(e + 26);
+    p.col_start = rd<uint16_t>(e + 28);
+    p.col_count = rd<uint16_t>(e + 30);
+    p.compression = e[42];
+    p.flags = e[43];
+    p.catalog_index = i;
+  }
+  // expert index (format.rs:144-154); an absent or truncated section leaves it empty, as the
+  // reference reader does (format.rs:286-291)
+  if (ei_off <= f->size && ei_size <= f->size - ei_off && ei_size > 0) {
+    const size_t n = (size_t)(ei_size / kExpertEntry);
+    for (size_t i = 0; i < n; i++) {
+      const uint8_t* e = h + ei_off + i * kExpertEntry;
+      const uint32_t key = (uint32_t)rd<uint16_t>(e + 0) << 16 | rd<uint16_t>(e + 2);
+      f->experts[key] = ExpertRange{rd<uint32_t>(e + 4), rd<uint32_t>(e + 8)};
+    }
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vib3_file_open(const char* path, vib3_file** out) {
+  if (!path || !out) return VIB3_ERR_BAD_POINTER;
+  *out = nullptr;
+  const int fd = open(path, O_RDONLY | O_CLOEXEC);
+  if (fd < 0) return VIB3_ERR_IO;
+  struct stat st;
+  if (fstat(fd, &st) != 0 || st.st_size <= 0) {
+    close(fd);
+    return VIB3_ERR_IO;
+  }
+  void* m = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+  if (m == MAP_FAILED) {
+    close(fd);
+    return VIB3_ERR_IO;
+  }
+  vib3_file* f = new (std::nothrow) vib3_file;
+  if (!f) {
+    munmap(m, (size_t)st.st_size);
+    close(fd);
+    return VIB3_ERR_IO;
+  }
+  f->fd = fd;
+  f->map = (const uint8_t*)m;
+  f->size = (size_t)st.st_size;
+  const int rc = parse(f);
+  if (rc) {
+    vib3_file_close(f);
+    return rc;
+  }
+  *out = f;
+  return 0;
+}
+
+void vib3_file_close(vib3_file* f) {
+  if (!f) return;
+  if (f->map) munmap((void*)f->map, f->size);
+  if (f->fd >= 0) close(f->fd);
+  delete f;
+}
+
+int vib3_file_get_info(const vib3_file* f, vib3_file_info* info) {
+  if (!f || !info) return VIB3_ERR_BAD_POINTER;
+  *info = f->info;
+  return 0;
+}
+
+int vib3_file_metadata(const vib3_file* f, const char** json, size_t* len) {
+  if (!f || !json || !len) return VIB3_ERR_BAD_POINTER;
+  *json = (const char*)f->metadata;
+  *len = f->metadata_size;
+  return 0;
+}
+
+int vib3_file_page(const vib3_file* f, uint32_t index, vib3_page_entry* entry) {
+  if (!f || !entry) return VIB3_ERR_BAD_POINTER;
+  if (index >= f->catalog.size()) return VIB3_ERR_BAD_COUNT;
+  *entry = f->catalog[index];
+  return 0;
+}
+
+int vib3_file_expert_pages(const vib3_file* f, uint16_t layer, uint16_t expert,
+                           vib3_page_entry* out, int max_entries, int* count) {
+  if (!f || !count || (max_entries > 0 && !out)) return VIB3_ERR_BAD_POINTER;
+  *count = 0;
+  auto it = f->experts.find((uint32_t)layer << 16 | expert);
+  if (it == f->experts.end()) return 0;
+  const ExpertRange r = it->second;
+  if ((uint64_t)r.first + r.count > f->catalog.size()) return VIB3_ERR_FORMAT;
+  *count = (int)r.count;
+  for (uint32_t i = 0; i < r.count && (int)i < max_entries; i++) out[i] = f->catalog[r.first + i];
+  return 0;
+}
+
+int vib3_file_page_data(const vib3_file* f, uint32_t index, const void** data, size_t* size) {
+  if (!f || !data || !size) return VIB3_ERR_BAD_POINTER;
+  if (index >= f->catalog.size()) return VIB3_ERR_BAD_COUNT;
+  const vib3_page_entry& p = f->catalog[index];
+  // LZ4 / zstd pages need the codec the reference links (lz4_flex, zstd); this build reads
+  // uncompressed pages only (format.rs:501-565, the COMPRESSION_NONE arm)
+  if (p.compression != 0) return VIB3_ERR_UNSUPPORTED;
+  if (p.file_offset > f->size || p.compressed_size > f->size - p.file_offset)
+    return VIB3_ERR_FORMAT;
+  *data = f->map + p.file_offset;
+  *size = p.compressed_size;
+  return 0;
+}
+
+int vib3_build_page_table(const vib3_file* f, uint16_t layer, const uint16_t* experts,
+                          int num_experts, const uint16_t segments[3],
+                          const uint64_t* page_addr, uint64_t* table, int max_pages,
+                          int rows_per_page[3]) {
+  if (!f || !experts || !segments || !page_addr || !table || !rows_per_page)
+    return VIB3_ERR_BAD_POINTER;
+  if (num_experts <= 0 || max_pages <= 0) return VIB3_ERR_BAD_COUNT;
+  memset(table, 0, sizeof(uint64_t) * (size_t)num_experts * 3 * max_pages);
+  int rpp[3] = {0, 0, 0};
+  for (int i = 0; i < num_experts; i++) {
+    auto it = f->experts.find((uint32_t)layer << 16 | experts[i]);
+    if (it == f->experts.end()) return VIB3_ERR_FORMAT;
+    const ExpertRange r = it->second;
+    for (int s = 0; s < 3; s++) {
+      int pages = 0;
+      for (uint32_t q = r.first; q < r.first + r.count && q < f->catalog.size(); q++) {
+        const vib3_page_entry& p = f->catalog[q];
+        if (p.segment != segments[s]) continue;
+        // the kernels address page p as rows [p * rows_per_page, ...): every page of a segment
+        // but the last holds the same number of rows, in page order (convert.rs:1852-1865); a
+        // short page elsewhere shows up as the next page's row_start
+        if (p.page_idx >= max_pages) return VIB3_ERR_BAD_COUNT;
+        if (rpp[s] == 0 && p.page_idx == 0) rpp[s] = p.row_count;
+        if (rpp[s] == 0 || p.row_start != (uint32_t)p.page_idx * (uint32_t)rpp[s] ||
+            p.row_count > rpp[s])
+          return VIB3_ERR_FORMAT;
+        table[((size_t)i * 3 + s) * max_pages + p.page_idx] = page_addr[q];
+        pages++;
+      }
+      if (pages == 0) return VIB3_ERR_FORMAT;
+      for (int p = 0; p < pages; p++)
+        if (!table[((size_t)i * 3 + s) * max_pages + p]) return VIB3_ERR_FORMAT;  // a gap
+    }
+  }
+  for (int s = 0; s < 3; s++) rows_per_page[s] = rpp[s];
+  return 0;
+}
+
+}  // extern "C"
