@@ -297,6 +297,155 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
   }
 }
 
+// ----------------------------------------------------------------------- matrix-core path, v2
+//
+// The same work items with the tokens' activations staged in LDS, so a wave can read long
+// pieces of few rows: a workgroup owns 64 weight rows (gate/up: 32 up + the same 32 gate rows;
+// down: 64 rows), one 16-row tile per wave, and walks k in steps of 1024. Per step each wave
+// loads 512 contiguous bytes of each of its 16 rows (lane (r, g) takes the 16-byte pieces
+// g, g + 4, ... of row r), the workgroup stages the 16 tokens' 1024 activations in LDS once, and
+// the wave runs 32 MFMAs against them. Loads of step s + 1 (weights into registers, activations
+// into the other LDS buffer) are issued before step s's matrix-core work.
+constexpr int kMx2K = 1024;                   // k per step
+constexpr int kMx2Pitch = kMx2K + 8;          // LDS row pitch (halves), against bank conflicts
+
+struct Mx2W {
+  uint4 w[8];     // 16 bytes of pieces g + 4j, j = 0..7, of this lane's row
+  uint4 sc[2];    // the row's 32 E8M0 scales of the step
+};
+
+template <bool GATEUP>
+__global__ __launch_bounds__(256) void k_mx_gemm2(MxArgs a) {
+  __shared__ uint16_t xs[2][kMxTokBlk][kMx2Pitch];
+  const int item = (int)blockIdx.y;
+  if (item >= *a.nitems) return;
+  const int tid = (int)threadIdx.x, lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rr = lane & 15, g = lane >> 4;
+  const int dix = a.it_d[item];
+  const int e = a.d_expert[dix], o_e = a.d_off[dix], t_e = a.d_cnt[dix];
+  const int p0 = a.it_p0[item] + (a.it_np[item] >> 8) * kMxTokBlk;
+
+  const int K = GATEUP ? a.hidden : a.inter;
+  const int M = GATEUP ? a.inter : a.hidden;
+  const int r0 = (int)blockIdx.x * (GATEUP ? 32 : 64);
+  if (p0 >= t_e) return;  // an empty fourth block of a 3-block chunk (uniform)
+  const size_t pkb = (size_t)K / 2, nsb = (size_t)K / 32;
+  // this wave's tile: gate/up waves 0, 1 = up rows r0 + 16w, waves 2, 3 = gate rows r0 + 16(w-2)
+  const int seg = GATEUP ? (wave < 2 ? 0 : 1) : 2;
+  const int row = GATEUP ? r0 + (wave & 1) * 16 + rr : r0 + wave * 16 + rr;
+  const uint8_t* base = (const uint8_t*)a.table[(size_t)e * 3 + seg];
+  const uint8_t* code = base + (size_t)row * pkb + (size_t)g * 16;
+  const uint8_t* scl = base + (size_t)M * pkb + (size_t)row * nsb;
+  // activation staging: thread t copies 64 halves (8 x 16 bytes) of token t / 16 of the block
+  const int st_tok = tid >> 4, st_part = tid & 15;
+  const int tk = p0 + st_tok;
+  const bool st_ok = tk < t_e;
+  const uint16_t* xrow =
+      GATEUP ? a.x + (size_t)a.ent_tok[o_e + (st_ok ? tk : p0)] * K
+             : a.h + (size_t)(o_e + (st_ok ? tk : p0)) * K;
+  xrow += st_part * 64;
+
+  auto load_w = [&](Mx2W& w, int k0) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) w.w[j] = ld16(code + k0 / 2 + j * 64);
+    w.sc[0] = ld16(scl + k0 / 32);
+    w.sc[1] = ld16(scl + k0 / 32 + 16);
+  };
+  auto load_x = [&](uint4 (&v)[8], int k0) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = ld16(xrow + k0 + j * 8);
+  };
+  auto store_x = [&](const uint4 (&v)[8], int b) {
+    uint4* d = (uint4*)&xs[b][st_tok][st_part * 64];
+#pragma unroll
+    for (int j = 0; j < 8; j++) d[j] = v[j];
+  };
+  f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const Mx2W& w, int b) {
+    const uint32_t scw[8] = {w.sc[0].x, w.sc[0].y, w.sc[0].z, w.sc[0].w,
+                             w.sc[1].x, w.sc[1].y, w.sc[1].z, w.sc[1].w};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      // piece g + 4j covers k = 128 j + 32 g .. + 31 of the step: E8M0 byte 4j + g
+      const float scale = e8m0_scale((uint8_t)(scw[j] >> (8 * g)));
+      const uint32_t words[4] = {w.w[j].x, w.w[j].y, w.w[j].z, w.w[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        bf16x8_t ab;
+        f16x8_t ah;
+        decode8<GATEUP>(words[q], scale, ab, ah);
+        const uint4 xb = *(const uint4*)&xs[b][rr][j * 128 + g * 32 + q * 8];
+        if (GATEUP)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, __builtin_bit_cast(bf16x8_t, xb), acc,
+                                                        0, 0, 0);
+        else
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, __builtin_bit_cast(f16x8_t, xb), acc,
+                                                       0, 0, 0);
+      }
+    }
+  };
+
+  const int nsteps = K / kMx2K;
+  Mx2W W0, W1;
+  uint4 xv[8];
+  load_w(W0, 0);
+  load_x(xv, 0);
+  store_x(xv, 0);
+  __syncthreads();
+  for (int s = 0;; s += 2) {
+    // step s from W0 / buffer 0, while step s + 1 loads into W1 / buffer 1
+    const bool more1 = s + 1 < nsteps;
+    if (more1) {
+      load_w(W1, (s + 1) * kMx2K);
+      load_x(xv, (s + 1) * kMx2K);
+    }
+    compute(W0, 0);
+    if (!more1) break;
+    store_x(xv, 1);
+    __syncthreads();
+    const bool more2 = s + 2 < nsteps;
+    if (more2) {
+      load_w(W0, (s + 2) * kMx2K);
+      load_x(xv, (s + 2) * kMx2K);
+    }
+    compute(W1, 1);
+    if (!more2) break;
+    store_x(xv, 0);
+    __syncthreads();
+  }
+
+  // epilogue: lane holds rows g*4 + i of the tile for token column rr
+  const int tok = p0 + rr;
+  if (GATEUP) {
+    // the gate tiles (waves 2, 3) meet the up tiles (waves 0, 1) through LDS
+    __syncthreads();
+    f32x4_t* ex = (f32x4_t*)&xs[0][0][0];
+    if (wave >= 2) ex[(wave - 2) * kWave + lane] = acc;
+    __syncthreads();
+    if (wave >= 2 || tok >= t_e) return;
+    const f32x4_t gt = ex[wave * kWave + lane];
+    uint16_t hv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float up = acc[i], gate = gt[i];
+      hv[i] = f32_to_f16_bits((gate / (1.0f + expf(-gate))) * up);  // kernels.rs:3041
+    }
+    const int orow = r0 + wave * 16 + g * 4;
+    *(uint2*)(a.h + (size_t)(o_e + tok) * M + orow) =
+        make_uint2((uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16));
+  } else {
+    if (tok >= t_e) return;
+    const int slot = a.ent_slot[o_e + tok];
+    uint16_t dv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) dv[i] = f32_to_f16_bits(acc[i]);
+    const int orow = r0 + wave * 16 + g * 4;
+    *(uint2*)(a.d + (size_t)slot * M + orow) =
+        make_uint2((uint32_t)dv[0] | ((uint32_t)dv[1] << 16), (uint32_t)dv[2] | ((uint32_t)dv[3] << 16));
+  }
+}
+
 // ----------------------------------------------------------------------------- row path
 //
 // Experts picked by at most kMxColdMax tokens (three quarters of the touched experts of a
@@ -566,6 +715,7 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
     *a.nitems = ipart[nt - 1];
     *a.ncold = cpart[nt - 1];
   }
+
   __syncthreads();
   // entry position = expert offset + number of earlier picks of the same expert
   for (int p = tid; p < a.n; p += nt) {
@@ -703,11 +853,21 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   a.h = (uint16_t*)(ws + w.h); a.d = (uint16_t*)(ws + w.d);
   a.hidden = B->hidden; a.inter = B->inter;
   const unsigned items = (unsigned)mx_max_items(B);
-  hipLaunchKernelGGL((k_mx_gemm<true, 4>), dim3((unsigned)(B->inter / 32), items), dim3(256), 0, st,
-                     a);
+  // matrix-core path: activations staged in LDS when k is a multiple of 1024, otherwise
+  // registers-only with k split over the waves (gate/up) or whole (down)
+  if (B->hidden % kMx2K == 0)
+    hipLaunchKernelGGL((k_mx_gemm2<true>), dim3((unsigned)(B->inter / 32), items), dim3(256), 0,
+                       st, a);
+  else
+    hipLaunchKernelGGL((k_mx_gemm<true, 4>), dim3((unsigned)(B->inter / 32), items), dim3(256), 0,
+                       st, a);
   mx_launch_rows<true>(a, B->hidden, st);
-  hipLaunchKernelGGL((k_mx_gemm<false, 1>), dim3((unsigned)(B->hidden / 256), items), dim3(256), 0, st,
-                     a);
+  if (B->inter % kMx2K == 0)
+    hipLaunchKernelGGL((k_mx_gemm2<false>), dim3((unsigned)(B->hidden / 64), items), dim3(256), 0,
+                       st, a);
+  else
+    hipLaunchKernelGGL((k_mx_gemm<false, 1>), dim3((unsigned)(B->hidden / 256), items), dim3(256),
+                       0, st, a);
   mx_launch_rows<false>(a, B->inter, st);
   hipLaunchKernelGGL(k_mx_combine, dim3((unsigned)((B->hidden + 255) / 256), (unsigned)B->tokens),
                      dim3(256), 0, st, (const uint16_t*)a.d, B->weights, B->ids,
