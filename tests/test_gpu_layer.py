@@ -206,6 +206,35 @@ def test_ragged_rows_per_page():
         check_layer(layer, bank, x, w.cpu().numpy(), O.F32, None, 0, 1.0, 3)
 
 
+@pytest.mark.parametrize("E,k,mode,shared", [
+    (256, 8, 0, 0),     # softmax top-8 over 256 (Qwen-style), fused routing
+    (512, 8, 1, 1),     # sigmoid top-8 over 512, the largest fused count
+    (300, 6, 0, 1),     # not a power of two (the reference's bitonic top-k needs one)
+    (640, 4, 1, 0),     # above 512: router launches of their own, then the selection
+])
+def test_router_counts(E, k, mode, shared):
+    """Expert counts either side of the fused-routing limit, softmax and sigmoid."""
+    from vib3_amd import moe
+    from vib3_amd._lib import DT_BF16
+    _say(f"case: router counts E={E} k={k} mode={mode} shared={shared}")
+    shape = moe.BankShape(hidden=512, inter=128, group_size=32, scale_dtype=DT_BF16,
+                          scale_sigma=0.05, num_experts=E, num_shared=shared)
+    bank = moe.Int4ExpertBank(shape, layer=6, seed=SEED)
+    w, bias = moe.make_router(shape, 6, SEED, 0.05, 0.1 if mode == 1 else None)
+    layer = moe.MoeInt4Layer(bank, w, bias, top_k=k, scoring_mode=mode,
+                             scaling_factor=2.5 if mode == 1 else 1.0, normalize=True)
+    assert _lib_fused(layer) == (E <= 512)
+    x = moe.make_activation(shape.hidden, E, SEED)
+    check_layer(layer, bank, x, w.cpu().numpy(), O.F32,
+                bias.cpu().numpy() if bias is not None else None, mode,
+                2.5 if mode == 1 else 1.0, k)
+
+
+def _lib_fused(layer):
+    from vib3_amd import _lib
+    return bool(_lib.load().vib3_moe_int4_router_fused(layer._desc(None)))
+
+
 def test_given_ids_without_router():
     """router_w == NULL: experts and weights come from the caller's device arrays (the shape of
     moe_experts_fused_gpu, kernels.cu:5868)."""
