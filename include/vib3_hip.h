@@ -288,6 +288,11 @@ int vib3_file_expert_pages(const vib3_file *file, uint16_t layer, uint16_t exper
 /* format.rs:501 read_page_sync for an uncompressed page: a pointer into the mapping and its
  * size. Compressed pages return VIB3_ERR_UNSUPPORTED (no LZ4/zstd codec in this build). */
 int vib3_file_page_data(const vib3_file *file, uint32_t index, const void **data, size_t *size);
+/* format.rs:501 read_page_sync: the page's bytes into a host buffer of `capacity` bytes,
+ * LZ4 pages (lz4_flex size-prepended blocks) decompressed; zstd pages return
+ * VIB3_ERR_UNSUPPORTED. *written = the page's raw size. */
+int vib3_file_read_page(const vib3_file *file, uint32_t index, void *dst, size_t capacity,
+                        size_t *written);
 
 /* The page table of vib3_moe_int4_layer from the catalog (engine.rs:1236-1299, one page per
  * segment there; any number here): for each experts[i] of `layer` and each of its segments

@@ -90,14 +90,46 @@ def test_errors(model, tmp_path):
     assert e.value.code == -5
 
 
-def test_compressed_pages_are_refused(tmp_path):
+def test_lz4_pages(tmp_path):
+    """LZ4 pages (lz4_flex's size-prepended blocks, format.rs:526) decompress to the raw page;
+    zstd pages are refused."""
     from vib3_amd._lib import Vib3Error
     from vib3_amd.vib3file import Vib3File
+    from vib3_writer import lz4_compress
     path = str(tmp_path / "lz4.vib3")
-    make_test_model(path, E=2, compressed={(0, 1, 2, 0)})
+    keys = {(0, 1, 2, 0), (0, 1, 0, 1), (0, 0xFFFF, 3, 0)}
+    _, dense = make_test_model(path, E=2, compressed=keys, zstd={(0, 0, 1, 0)})
+    want = {(p[0], p[1], p[2], p[3]): p[7] for p in dense["pages"]}
     with Vib3File(path) as f:
-        p = [q for q in f.expert_pages(0, 1) if q.segment == 2][0]
-        assert p.compression == 1
-        with pytest.raises(Vib3Error) as e:
-            f.page_bytes(p.catalog_index)
-        assert e.value.code == -1
+        seen = 0
+        for e in (0, 1, 0xFFFF):
+            for p in f.expert_pages(0, e):
+                k = (p.layer, p.expert, p.segment, p.page_idx)
+                if k == (0, 0, 1, 0):
+                    assert p.compression == 2
+                    with pytest.raises(Vib3Error) as err:
+                        f.page_bytes(p.catalog_index)
+                    assert err.value.code == -1
+                    continue
+                assert p.compression == (1 if k in keys else 0)
+                seen += p.compression == 1
+                assert f.page_bytes(p.catalog_index).tobytes() == want[k]
+        assert seen == 3
+    # pages that do compress: long runs (overlapping matches, extended lengths), short
+    # repeats, literal runs over 15 bytes, and tiny pages, through the library's decompressor
+    rng = np.random.default_rng(3)
+    datas = [b"a" * 1000, b"", b"abc", bytes(rng.integers(0, 4, 5000, dtype=np.uint8)),
+             bytes(rng.integers(0, 256, 3000, dtype=np.uint8)) * 3,
+             b"".join(bytes([i % 7]) * (i % 40 + 1) for i in range(400))]
+    from vib3_writer import write_vib3
+    cfg = {"num_layers": 1, "num_experts": 1, "num_active_experts": 1, "hidden_dim": 64,
+           "expert_hidden_dim": 64, "_expert_dtype_code": 5, "_shared_dtype_code": 0}
+    pages = [(0, 0, 0, i, 0, 1, 1, d) for i, d in enumerate(datas)]
+    path2 = str(tmp_path / "runs.vib3")
+    write_vib3(path2, cfg, pages, compressed={(0, 0, 0, i) for i in range(len(datas))})
+    with Vib3File(path2) as f:
+        for p in f.expert_pages(0, 0):
+            assert p.compression == 1
+            assert f.page_bytes(p.catalog_index).tobytes() == datas[p.page_idx]
+        ratio = f.expert_pages(0, 0)[0].compressed_size / 1000
+        assert ratio < 0.05

@@ -14,12 +14,68 @@ MAGIC = 0x3342495600000001
 PAGE_SIZE = 2 * 1024 * 1024
 
 
-def write_vib3(path, config: dict, pages, compressed=()):
+def lz4_compress(data: bytes) -> bytes:
+    """A greedy LZ4 block compressor (4-byte hash matches) in lz4_flex's size-prepended form:
+    little-endian raw size, then sequences; the last 5 bytes are literals and no match starts
+    in the last 12 (the LZ4 block format's end rules)."""
+    data = bytes(data)
+    n = len(data)
+    out = bytearray(struct.pack("<I", n))
+    table = {}
+    i = anchor = 0
+    limit = n - 12
+
+    def length_bytes(v):
+        b = bytearray()
+        while v >= 255:
+            b.append(255)
+            v -= 255
+        b.append(v)
+        return b
+
+    def emit(lit, mlen, off):
+        tok_l = min(len(lit), 15)
+        tok_m = 0 if mlen is None else min(mlen - 4, 15)
+        out.append((tok_l << 4) | tok_m)
+        if tok_l == 15:
+            out.extend(length_bytes(len(lit) - 15))
+        out.extend(lit)
+        if mlen is not None:
+            out.extend(struct.pack("<H", off))
+            if tok_m == 15:
+                out.extend(length_bytes(mlen - 4 - 15))
+
+    while i < limit:
+        key = data[i:i + 4]
+        cand = table.get(key)
+        table[key] = i
+        if cand is not None and i - cand <= 0xFFFF:
+            m = 4
+            while i + m < n - 5 and data[cand + m] == data[i + m]:
+                m += 1
+            emit(data[anchor:i], m, i - cand)
+            i += m
+            anchor = i
+        else:
+            i += 1
+    emit(data[anchor:], None, 0)
+    return bytes(out)
+
+
+def write_vib3(path, config: dict, pages, compressed=(), zstd=()):
     """pages: iterable of (layer, expert, segment, page_idx, row_start, row_count, col_count,
-    data bytes). `compressed`: (layer, expert, segment, page_idx) keys to flag as LZ4 (their
-    bytes are stored as given, for the reader's error path)."""
+    data bytes). Pages whose (layer, expert, segment, page_idx) is in `compressed` are stored
+    LZ4-compressed (compression 1); those in `zstd` are only flagged 2 (for the reader's
+    refusal path)."""
     meta = json.dumps(config, indent=2).encode()
-    pages = sorted(pages, key=lambda p: (p[0], p[1], p[2], p[3]))
+    stored = []
+    for p in pages:
+        key = (p[0], p[1], p[2], p[3])
+        if key in compressed:
+            stored.append((*p[:7], lz4_compress(p[7]), 1, len(p[7])))
+        else:
+            stored.append((*p, 2 if key in zstd else 0, len(p[7])))
+    pages = sorted(stored, key=lambda p: (p[0], p[1], p[2], p[3]))
     cat_off = 512 + len(meta)
     cat_size = 48 * len(pages)
     experts = {}
@@ -49,14 +105,13 @@ def write_vib3(path, config: dict, pages, compressed=()):
     header += bytes(354)
     catalog = b""
     for p, off in zip(pages, offs):
-        layer, expert, seg, idx, r0, rc, cc, data = p
-        comp = 1 if (layer, expert, seg, idx) in compressed else 0
+        layer, expert, seg, idx, r0, rc, cc, data, comp, raw = p
         catalog += struct.pack("<HHHHQIIHHHHffHBB4x", layer, expert, seg, idx, off, len(data),
-                               len(data), r0, rc, 0, cc, 0.0, 0.0, 0, comp, 0)
+                               raw, r0, rc, 0, cc, 0.0, 0.0, 0, comp, 0)
     index = b""
     for (layer, expert), idx in sorted(experts.items()):
         index += struct.pack("<HHIIIHH", layer, expert, idx[0], len(idx),
-                             sum(len(pages[i][7]) for i in idx),
+                             sum(pages[i][9] for i in idx),
                              len({pages[i][2] for i in idx}), 0)
     with open(path, "wb") as f:
         f.write(header + meta + catalog + index)
@@ -94,7 +149,7 @@ def dense_pages(layer, expert, segment, raw: bytes, row_bytes, rows_per_page):
 
 def make_test_model(path, seed=0x5EED0007, hidden=1024, inter=256, E=8, top_k=2,
                     gu_rows_per_page=96, down_rows_per_page=400, router_rows_per_page=3,
-                    with_shared=True, compressed=()):
+                    with_shared=True, compressed=(), zstd=()):
     """A one-layer INT4 MoE model file (Kimi-style: sigmoid router with scaling, one shared
     expert with a sigmoid gate, pre-MoE norm) from the oracle's seeded generator. Returns the
     config and the dense tensors (router / norm / gate f16 bits) for the checks."""
@@ -128,5 +183,5 @@ def make_test_model(path, seed=0x5EED0007, hidden=1024, inter=256, E=8, top_k=2,
     pages += dense_pages(0, 0xFFFF, 7, norm.tobytes(), hidden * 2, 1)
     if with_shared:
         pages += dense_pages(0, 0xFFFF, 26, gate.tobytes(), hidden * 2, 1)
-    write_vib3(path, cfg, pages, compressed=compressed)
+    write_vib3(path, cfg, pages, compressed=compressed, zstd=zstd)
     return cfg, {"router": router, "norm": norm, "gate": gate, "pages": pages}

@@ -97,6 +97,7 @@ SIGNATURES = {
     "vib3_file_page": (I, [P, C.c_uint32, P]),
     "vib3_file_expert_pages": (I, [P, C.c_uint16, C.c_uint16, P, I, P]),
     "vib3_file_page_data": (I, [P, C.c_uint32, P, P]),
+    "vib3_file_read_page": (I, [P, C.c_uint32, P, S, P]),
     "vib3_build_page_table": (I, [P, C.c_uint16, P, I, P, P, P, I, P]),
     "vib3_hip_version": (C.c_char_p, []),
 }

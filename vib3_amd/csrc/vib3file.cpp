@@ -203,6 +203,68 @@ int vib3_file_page_data(const vib3_file* f, uint32_t index, const void** data, s
   return 0;
 }
 
+// LZ4 block decompression of lz4_flex's size-prepended frame (format.rs:526-533): a 4-byte
+// little-endian decompressed size, then LZ4 sequences: a token (literal count in the high
+// nibble, match length - 4 in the low one, 15 = more bytes follow, each adding up to 255),
+// the literals, a 2-byte little-endian match offset and the extra match-length bytes; the
+// last sequence has literals only. Every read and write is bounds-checked.
+static int lz4_decompress(const uint8_t* src, size_t n, uint8_t* dst, size_t cap,
+                          size_t* written) {
+  if (n < 4) return VIB3_ERR_FORMAT;
+  const size_t want = (size_t)rd<uint32_t>(src);
+  if (want > cap) return VIB3_ERR_BAD_COUNT;
+  size_t i = 4, o = 0;
+  auto extend = [&](size_t& len) {
+    uint8_t b;
+    do {
+      if (i >= n) return false;
+      b = src[i++];
+      len += b;
+    } while (b == 255);
+    return true;
+  };
+  while (i < n) {
+    const uint8_t token = src[i++];
+    size_t lit = token >> 4;
+    if (lit == 15 && !extend(lit)) return VIB3_ERR_FORMAT;
+    if (lit > n - i || lit > want - o) return VIB3_ERR_FORMAT;
+    memcpy(dst + o, src + i, lit);
+    i += lit;
+    o += lit;
+    if (i == n) break;  // the last sequence: literals only
+    if (n - i < 2) return VIB3_ERR_FORMAT;
+    const size_t off = rd<uint16_t>(src + i);
+    i += 2;
+    size_t len = (token & 15);
+    if (len == 15 && !extend(len)) return VIB3_ERR_FORMAT;
+    len += 4;
+    if (off == 0 || off > o || len > want - o) return VIB3_ERR_FORMAT;
+    for (size_t k = 0; k < len; k++, o++) dst[o] = dst[o - off];  // may overlap itself
+  }
+  if (o != want) return VIB3_ERR_FORMAT;
+  *written = o;
+  return 0;
+}
+
+int vib3_file_read_page(const vib3_file* f, uint32_t index, void* dst, size_t capacity,
+                        size_t* written) {
+  if (!f || !dst || !written) return VIB3_ERR_BAD_POINTER;
+  if (index >= f->catalog.size()) return VIB3_ERR_BAD_COUNT;
+  const vib3_page_entry& p = f->catalog[index];
+  if (p.file_offset > f->size || p.compressed_size > f->size - p.file_offset)
+    return VIB3_ERR_FORMAT;
+  const uint8_t* src = f->map + p.file_offset;
+  if (p.compression == 0) {  // COMPRESSION_NONE
+    const size_t n = p.compressed_size < capacity ? p.compressed_size : capacity;
+    memcpy(dst, src, n);
+    *written = n;
+    return 0;
+  }
+  if (p.compression == 1)  // COMPRESSION_LZ4
+    return lz4_decompress(src, p.compressed_size, (uint8_t*)dst, capacity, written);
+  return VIB3_ERR_UNSUPPORTED;  // zstd: no codec in this build
+}
+
 int vib3_build_page_table(const vib3_file* f, uint16_t layer, const uint16_t* experts,
                           int num_experts, const uint16_t segments[3],
                           const uint64_t* page_addr, uint64_t* table, int max_pages,

@@ -101,7 +101,15 @@ class Vib3File:
         return list(out[: n.value])
 
     def page_bytes(self, index: int) -> np.ndarray:
-        """An uncompressed page's bytes (a read-only view of the mapping)."""
+        """A page's bytes: a read-only view of the mapping, or the decompressed copy of an LZ4
+        page (format.rs:501 read_page_sync)."""
+        e = self.page(index)
+        if e.compression != 0:
+            out = np.empty(e.raw_size, dtype=np.uint8)
+            n = C.c_size_t()
+            _check("vib3_file_read_page", self._lib.vib3_file_read_page(
+                self._h, index, out.ctypes.data, out.size, C.byref(n)))
+            return out[: n.value]
         p, n = C.c_void_p(), C.c_size_t()
         _check("vib3_file_page_data",
                self._lib.vib3_file_page_data(self._h, index, C.byref(p), C.byref(n)))
