@@ -199,7 +199,7 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
   const int rpw = GATEUP ? 32 : 64;                 // rows of each matrix per wave
   const int kw = wave % KS;                          // this wave's share of the k steps
   const int r0 = (int)blockIdx.x * rpw * (4 / KS) + (wave / KS) * rpw;
-  if (r0 >= M || p0 >= t_e) return;                  // uniform over the workgroup when KS > 1
+  if (r0 >= M || p0 >= t_e) return;                  // (a guard; uniform when KS > 1)
   const size_t pkb = (size_t)K / 2, nsb = (size_t)K / 32;
   const uint8_t* m0 = (const uint8_t*)a.table[(size_t)e * 3 + (GATEUP ? 0 : 2)];
   const uint8_t* m1 = GATEUP ? (const uint8_t*)a.table[(size_t)e * 3 + 1] : m0;
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
 
 // ----------------------------------------------------------------------- matrix-core path, v2
 //
-// The same work items with the tokens' activations staged in LDS, so a wave can read long
+// The work items above with the tokens' activations staged in LDS, so a wave can read long
 // pieces of few rows: a workgroup owns 64 weight rows (gate/up: 32 up + the same 32 gate rows;
 // down: 64 rows), one 16-row tile per wave, and walks k in steps of 1024. Per step each wave
 // loads 512 contiguous bytes of each of its 16 rows (lane (r, g) takes the 16-byte pieces
@@ -329,7 +329,7 @@ __global__ __launch_bounds__(256) void k_mx_gemm2(MxArgs a) {
   const int K = GATEUP ? a.hidden : a.inter;
   const int M = GATEUP ? a.inter : a.hidden;
   const int r0 = (int)blockIdx.x * (GATEUP ? 32 : 64);
-  if (p0 >= t_e) return;  // an empty fourth block of a 3-block chunk (uniform)
+  if (p0 >= t_e) return;  // (a guard; uniform)
   const size_t pkb = (size_t)K / 2, nsb = (size_t)K / 32;
   // this wave's tile: gate/up waves 0, 1 = up rows r0 + 16w, waves 2, 3 = gate rows r0 + 16(w-2)
   const int seg = GATEUP ? (wave < 2 ? 0 : 1) : 2;
@@ -396,9 +396,9 @@ __global__ __launch_bounds__(256) void k_mx_gemm2(MxArgs a) {
   for (int s = 0;; s += 2) {
     // step s from W0 / buffer 0, while step s + 1 loads into W1 / buffer 1
     const bool more1 = s + 1 < nsteps;
-    if (more1) {
-      load_w(W1, (s + 1) * kMx2K);
+    if (more1) {  // activations first: waiting for them must not wait for these weights
       load_x(xv, (s + 1) * kMx2K);
+      load_w(W1, (s + 1) * kMx2K);
     }
     compute(W0, 0);
     if (!more1) break;
@@ -406,8 +406,8 @@ __global__ __launch_bounds__(256) void k_mx_gemm2(MxArgs a) {
     __syncthreads();
     const bool more2 = s + 2 < nsteps;
     if (more2) {
-      load_w(W0, (s + 2) * kMx2K);
       load_x(xv, (s + 2) * kMx2K);
+      load_w(W0, (s + 2) * kMx2K);
     }
     compute(W1, 1);
     if (!more2) break;
@@ -615,10 +615,8 @@ __global__ __launch_bounds__(256) void k_mx_rows(MxArgs a) {
   }
 }
 
-// Token blocks of a chunk of c tokens (1 <= c <= 64), rounded up to a divisor of 4.
-__host__ __device__ constexpr int mx_chunk_blocks(int c) {
-  return c <= kMxTokBlk ? 1 : c <= 2 * kMxTokBlk ? 2 : 4;
-}
+// Token blocks of a chunk of c tokens (1 <= c <= 64).
+__host__ __device__ constexpr int mx_chunk_blocks(int c) { return (c + kMxTokBlk - 1) / kMxTokBlk; }
 
 // Work items of an expert with c entries: one per part of each 64-token chunk.
 __host__ __device__ inline int mx_expert_items(int c) {
@@ -769,9 +767,8 @@ struct MxWs {
       h, d, total;
 };
 
-// Upper bound of the work items. A chunk of c tokens has ceil(c / 16) blocks, plus one when
-// 3 blocks round up to 4: at most n / 16 + 2 per chunk, and there are at most
-// min(E, n) + n / 64 chunks.
+// Upper bound of the work items: a chunk of c tokens has ceil(c / 16) blocks, at most
+// n / 16 + 1 per chunk, and there are at most min(E, n) + n / 64 chunks (a bound with room).
 static int mx_max_items(const vib3_moe_mxfp4_batch* B) {
   const int n = B->tokens * B->top_k;
   return n / kMxTokBlk + 2 * ((B->num_experts < n ? B->num_experts : n) + n / kMxChunk);
@@ -863,8 +860,8 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
                        st, a);
   mx_launch_rows<true>(a, B->hidden, st);
   if (B->inter % kMx2K == 0)
-    hipLaunchKernelGGL((k_mx_gemm2<false>), dim3((unsigned)(B->hidden / 64), items), dim3(256), 0,
-                       st, a);
+    hipLaunchKernelGGL((k_mx_gemm2<false>), dim3((unsigned)(B->hidden / 64), items), dim3(256),
+                       0, st, a);
   else
     hipLaunchKernelGGL((k_mx_gemm<false, 1>), dim3((unsigned)(B->hidden / 256), items), dim3(256),
                        0, st, a);
