@@ -299,6 +299,7 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
       !aligned16(L->workspace))
     return VIB3_ERR_BAD_POINTER;
   if (L->norm_weight && L->x_dtype != VIB3_DT_F32) return VIB3_ERR_UNSUPPORTED;  // f32 stream
+  if ((L->norm_weight || L->shared_gate) && L->hidden > 8192) return VIB3_ERR_UNSUPPORTED;
   if (L->shared_gate && L->num_shared <= 0) return VIB3_ERR_BAD_COUNT;
   const LayerWs w = layer_ws(L);
   if (L->workspace_bytes < w.total) return VIB3_ERR_WORKSPACE;
