@@ -104,6 +104,20 @@ def test_small_batches_match_oracle(hidden, inter, E, T, k):
     _say(f"[mxfp4]   bf16 outputs equal to the oracle's: {same:.4f}")
 
 
+def test_largest_batch():
+    """The most picks one launch takes (tokens x top_k = 4096: 512 tokens x 8), every token
+    against the oracle on a small shape."""
+    _say("[mxfp4] largest batch: 512 tokens x top-8 over 48 experts")
+    from vib3_amd.mxfp4 import zipf_picks
+    hidden, inter, E, T, k = 256, 256, 48, 512, 8
+    bank = _bank(hidden, inter, E, layer=7)
+    ids, w = zipf_picks(T, E, k, s=1.1, seed=SEED + 7)
+    x, xh = _x(T, hidden, stream=78)
+    got = _run(bank, x, ids, w)
+    ref = _oracle(bank, xh, ids, w)
+    _check(got, ref)
+
+
 def test_out_of_range_ids_are_skipped():
     _say("[mxfp4] out-of-range ids")
     hidden, inter, E, T, k = 256, 256, 5, 4, 3

@@ -47,7 +47,7 @@ struct MxArgs {
   const int* nd;              // number of distinct experts
   const int* it_d;            // [items] distinct index of each work item
   const int* it_p0;           // [items] first entry of the item's token chunk within its expert
-  const int* it_np;           // [items] token blocks of the chunk (1, 2, 4) | part << 8
+  const int* it_np;           // [items] token blocks of the chunk (1..4) | part << 8
   const int* nitems;
   const int* ent_tok;         // [T*top_k] token of each entry (grouped by expert)
   const int* ent_slot;        // [T*top_k] t*top_k + j of each entry
@@ -180,7 +180,7 @@ __device__ __forceinline__ void mx_pass(const uint8_t* const (&tcode)[kMxTiles],
 // rather than one piece of each of 128 rows, and the four partial tiles are summed through
 // LDS in wave order. With KS = 1 (down, k = 2048 is only 8 steps) the waves take 4 adjacent
 // row blocks and each runs its whole k range. The token blocks of one 64-token chunk are
-// adjacent items, gridDim.x (a multiple of 8) workgroups apart: the same XCD and L2, close in
+// adjacent items, gridDim.x (for gate/up a multiple of 8) workgroups apart: the same XCD and L2, close in
 // time, so HBM serves their shared weight lines once.
 template <bool GATEUP, int KS>
 __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
