@@ -730,16 +730,55 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
 __global__ __launch_bounds__(256) void k_mx_combine(const uint16_t* d, const float* w,
                                                       const uint16_t* ids, int E, uint16_t* out,
                                                       int hidden, int top_k) {
+  // thread: 8 consecutive outputs of token t. Each group of up to 8 picks has all its loads
+  // (ids, weights, 16-byte rows of d) issued before any is used: one round trip per group
+  // instead of one per pick.
   const int t = (int)blockIdx.y;
-  const int r = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (r >= hidden) return;
-  float o = 0.0f;
-  for (int j = 0; j < top_k; j++) {
-    const size_t slot = (size_t)t * top_k + j;
-    if (ids[slot] >= E) continue;
-    o = add_mul_rn(o, w[slot], f16_to_f32(d[slot * hidden + r]));
+  const int r0 = (int)(blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (r0 >= hidden) return;
+  const bool vec = hidden % 8 == 0 && ((uintptr_t)out & 15) == 0;  // d: the aligned workspace
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < top_k; j0 += 8) {
+    uint16_t id[8];
+    float wt[8];
+    uint4 dv[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const size_t slot = (size_t)t * top_k + min(j0 + q, top_k - 1);
+      id[q] = ids[slot];
+      wt[q] = w[slot];
+      if (vec) {
+        dv[q] = *(const uint4*)(d + slot * hidden + r0);
+      } else {
+        uint16_t h[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = r0 + i < hidden ? d[slot * hidden + r0 + i] : 0;
+        dv[q] = make_uint4(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16,
+                           h[4] | (uint32_t)h[5] << 16, h[6] | (uint32_t)h[7] << 16);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      if (j0 + q >= top_k || id[q] >= E) continue;  // picks past E are skipped
+      const uint32_t v[4] = {dv[q].x, dv[q].y, dv[q].z, dv[q].w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        o[2 * i] = add_mul_rn(o[2 * i], wt[q], f16_to_f32((uint16_t)(v[i] & 0xffff)));
+        o[2 * i + 1] = add_mul_rn(o[2 * i + 1], wt[q], f16_to_f32((uint16_t)(v[i] >> 16)));
+      }
+    }
   }
-  out[(size_t)t * hidden + r] = f32_to_bf16_bits(o);
+  // o = o + w * d in pick order per output, as weighted_accumulate_f32 (kernels.rs:2000)
+  uint16_t b[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) b[i] = f32_to_bf16_bits(o[i]);
+  if (vec) {
+    *(uint4*)(out + (size_t)t * hidden + r0) =
+        make_uint4(b[0] | (uint32_t)b[1] << 16, b[2] | (uint32_t)b[3] << 16,
+                   b[4] | (uint32_t)b[5] << 16, b[6] | (uint32_t)b[7] << 16);
+  } else {
+    for (int i = 0; i < 8 && r0 + i < hidden; i++) out[(size_t)t * hidden + r0 + i] = b[i];
+  }
 }
 
 // Row-path launch: K = the reduction length picks the chunks per lane (K <= 8192).
@@ -866,7 +905,7 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
     hipLaunchKernelGGL((k_mx_gemm<false, 1>), dim3((unsigned)(B->hidden / 256), items), dim3(256),
                        0, st, a);
   mx_launch_rows<false>(a, B->inter, st);
-  hipLaunchKernelGGL(k_mx_combine, dim3((unsigned)((B->hidden + 255) / 256), (unsigned)B->tokens),
+  hipLaunchKernelGGL(k_mx_combine, dim3((unsigned)((B->hidden + 2047) / 2048), (unsigned)B->tokens),
                      dim3(256), 0, st, (const uint16_t*)a.d, B->weights, B->ids,
                      B->num_experts, (uint16_t*)B->out, B->hidden, B->top_k);
   VIB3_RETURN_LAUNCH();
