@@ -670,23 +670,40 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
     is += cnt[e] > kMxColdMax ? mx_expert_items(cnt[e]) : 0;
     cs += cnt[e] > 0 && cnt[e] <= kMxColdMax;
   }
-  part[tid] = s;
-  dpart[tid] = ds;
-  ipart[tid] = is;
-  cpart[tid] = cs;
-  __syncthreads();
-  for (int st = 1; st < nt; st <<= 1) {  // Hillis-Steele inclusive scans
-    const int v = tid >= st ? part[tid - st] : 0;
-    const int dv = tid >= st ? dpart[tid - st] : 0;
-    const int iv = tid >= st ? ipart[tid - st] : 0;
-    const int cv = tid >= st ? cpart[tid - st] : 0;
-    __syncthreads();
-    part[tid] += v;
-    dpart[tid] += dv;
-    ipart[tid] += iv;
-    cpart[tid] += cv;
-    __syncthreads();
+  // inclusive scans of the four counts over the workgroup: within each wave by lane shuffles,
+  // then over the (at most 16) wave totals, with two barriers in all
+  int sc[4] = {s, ds, is, cs};
+  const int lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+  for (int st = 1; st < 64; st <<= 1) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int v = __shfl_up(sc[q], st, 64);
+      if (lane >= st) sc[q] += v;
+    }
   }
+  __shared__ int wtot[16][4];
+  if (lane == 63) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) wtot[wv][q] = sc[q];
+  }
+  __syncthreads();
+  if (tid < 4) {  // thread q scans the wave totals of count q
+    int acc = 0;
+    for (int w = 0; w < nt / 64; w++) {
+      const int v = wtot[w][tid];
+      wtot[w][tid] = acc;  // exclusive: what the waves before w hold
+      acc += v;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 4; q++) sc[q] += wtot[wv][q];
+  part[tid] = sc[0];
+  dpart[tid] = sc[1];
+  ipart[tid] = sc[2];
+  cpart[tid] = sc[3];
+  __syncthreads();  // the last thread's totals are read below
   int run = part[tid] - s, drun = dpart[tid] - ds, irun = ipart[tid] - is, crun = cpart[tid] - cs;
   for (int e = e0; e < e1; e++) {
     off[e] = run;
