@@ -280,7 +280,8 @@ int vib3_build_page_table(const vib3_file* f, uint16_t layer, const uint16_t* ex
     const ExpertRange r = it->second;
     for (int s = 0; s < 3; s++) {
       int pages = 0;
-      for (uint32_t q = r.first; q < r.first + r.count && q < f->catalog.size(); q++) {
+      const uint64_t qend = std::min<uint64_t>((uint64_t)r.first + r.count, f->catalog.size());
+      for (uint64_t q = r.first; q < qend; q++) {
         const vib3_page_entry& p = f->catalog[q];
         if (p.segment != segments[s]) continue;
         // the kernels address page p as rows [p * rows_per_page, ...): every page of a segment
@@ -291,12 +292,15 @@ int vib3_build_page_table(const vib3_file* f, uint16_t layer, const uint16_t* ex
         if (rpp[s] == 0 || p.row_start != (uint32_t)p.page_idx * (uint32_t)rpp[s] ||
             p.row_count > rpp[s])
           return VIB3_ERR_FORMAT;
-        table[((size_t)i * 3 + s) * max_pages + p.page_idx] = page_addr[q];
+        uint64_t& slot = table[((size_t)i * 3 + s) * max_pages + p.page_idx];
+        if (slot) return VIB3_ERR_FORMAT;  // the same page twice
+        slot = page_addr[q];
+        if (!slot) return VIB3_ERR_FORMAT;  // not resident
         pages++;
       }
       if (pages == 0) return VIB3_ERR_FORMAT;
-      for (int p = 0; p < pages; p++)
-        if (!table[((size_t)i * 3 + s) * max_pages + p]) return VIB3_ERR_FORMAT;  // a gap
+      for (int p = 0; p < pages; p++)  // distinct pages, each below max_pages: no gap allowed
+        if (!table[((size_t)i * 3 + s) * max_pages + p]) return VIB3_ERR_FORMAT;
     }
   }
   for (int s = 0; s < 3; s++) rows_per_page[s] = rpp[s];
