@@ -156,6 +156,32 @@ def test_layer_with_norm_gate_residual(hidden, inter, E, k, ns, layout, use_norm
     assert rel <= 1e-3
 
 
+def test_in_place_residual_stream():
+    """The engine's in-place form (engine.rs:5302): x, residual and out all the same f32
+    hidden_state buffer. The result equals the out-of-place launch bit for bit."""
+    from vib3_amd import moe
+    from vib3_amd._lib import DT_BF16, ROUTER_SIGMOID
+    _say("case: in-place residual stream")
+    sh = _shape(moe, DT_BF16, 1024, 256, 16, 1)
+    bank = moe.Int4ExpertBank(sh, layer=4, seed=SEED)
+    w, bias = moe.make_router(sh, 4, SEED, 0.02, 0.1)
+    layer = moe.MoeInt4Layer(bank, w, bias, top_k=4, scoring_mode=ROUTER_SIGMOID,
+                             scaling_factor=2.827, norm_weight=_dev16(_f16(1024, 10, 0.1, 1.0)),
+                             shared_gate=_dev16(_f16(1024, 11, 0.02)))
+    xh = _f32(1024, 14, 20.0)
+    ref = layer.launch(torch.from_numpy(xh).cuda(),
+                       residual=torch.from_numpy(xh).cuda()).cpu().numpy().copy()
+    hs = torch.from_numpy(xh.copy()).cuda()
+    d = layer._desc(hs)
+    d.residual = hs.data_ptr()
+    d.out = hs.data_ptr()
+    from vib3_amd import _lib
+    assert _lib.load().vib3_launch_moe_int4_layer(
+        d, torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(hs.cpu().numpy(), ref)
+
+
 def test_norm_needs_f32_stream():
     from vib3_amd import moe
     from vib3_amd._lib import DT_BF16, ROUTER_SIGMOID, Vib3Error
