@@ -1,5 +1,6 @@
 """Write tests/golden/fixtures.npz: small known-answer cases for the INT4 GEMV, the fused SwiGLU,
-the router top-k, a small MoE layer and a batched MXFP4 MoE.
+the router top-k, a small MoE layer, a batched MXFP4 MoE, and the pre-MoE RMSNorm with the
+shared expert's sigmoid gate.
 
 Inputs are not stored: they come from the counter-based generator (seed, stream) shared by the
 oracle (oracle/cpu_ref.c) and the device (vib3_amd/csrc/synth.hip), so a fixture holds the
@@ -153,6 +154,24 @@ def main() -> None:
     fx["mxfp4_ids"], fx["mxfp4_wts"] = mids.astype(np.int64), mw
     meta["mxfp4"] = dict(hidden=hidden, inter=inter, E=E, tokens=T, top_k=k2,
                          page_streams="200 + 3*e + segment", x=(SEED, 9, "bf16"))
+
+    # pre-MoE RMSNorm (kernels.cu:921) of an f32 residual-stream vector with f16 weights, and
+    # the shared expert's sigmoid gate on the result (kernels.rs:3630, kernels.cu:2114)
+    n = 1000
+    xr = O.synth_normal_array(SEED, 30, 0, n, 20.0, O.F32)
+    nw = (O.synth_normal_array(SEED, 31, 0, n, 0.1, O.F32) + np.float32(1.0)).astype(np.float16)
+    gw = O.synth_normal_array(SEED, 32, 0, n, 0.02, O.F16)
+    y = O.rms_norm_f32(xr, nw.view(np.uint16), 1e-6)
+    x64 = xr.astype(np.float64)
+    ref = x64 / np.sqrt(np.mean(x64 * x64) + 1e-6) * nw.astype(np.float64)
+    assert np.max(np.abs(y - ref)) <= 4e-7 * np.max(np.abs(ref))
+    gate = O.sigmoid(O.linear_row_f16(y, gw))
+    gref = 1 / (1 + np.exp(-np.dot(y.astype(np.float64), gw.view(np.float16).astype(np.float64))))
+    assert abs(gate - gref) <= 1e-6
+    fx["rmsnorm_out"] = y
+    fx["rmsnorm_gate"] = np.array([gate], dtype=np.float32)
+    meta["rmsnorm"] = dict(n=n, eps=1e-6, x=(SEED, 30, 20.0), w=(SEED, 31, 0.1, 1.0),
+                           gate=(SEED, 32, 0.02))
 
     np.savez(OUT, meta=np.array(json.dumps(meta)), **fx)
     print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes)")

@@ -95,3 +95,18 @@ def test_mxfp4_fixture():
     out = O.moe_mxfp4_batched(x.reshape(m["tokens"], m["hidden"]), m["hidden"], m["inter"], pages,
                               f["mxfp4_ids"].astype(np.uint16), f["mxfp4_wts"])
     assert np.array_equal(out, f["mxfp4_out_bf16"])
+
+
+def test_rmsnorm_fixture():
+    f, meta = load()
+    m = meta["rmsnorm"]
+    seed, stream, sigma = m["x"]
+    x = O.synth_normal_array(seed, stream, 0, m["n"], sigma, O.F32)
+    wseed, wstream, wsigma, woff = m["w"]
+    w = (O.synth_normal_array(wseed, wstream, 0, m["n"], wsigma, O.F32) + np.float32(woff)).astype(
+        np.float16)
+    y = O.rms_norm_f32(x, w.view(np.uint16), m["eps"])
+    assert np.array_equal(y, f["rmsnorm_out"])
+    gseed, gstream, gsigma = m["gate"]
+    gw = O.synth_normal_array(gseed, gstream, 0, m["n"], gsigma, O.F16)
+    assert np.float32(O.sigmoid(O.linear_row_f16(y, gw))) == f["rmsnorm_gate"][0]

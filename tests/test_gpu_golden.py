@@ -177,3 +177,22 @@ def test_mxfp4_fixture():
     for t in range(T):
         assert rel_l2(got[t], ref[t]) <= 1e-3, t
     assert np.mean(got_bits == ref_bits) > 0.97
+
+
+def test_rmsnorm_fixture():
+    """vib3_launch_rms_norm_f32 against the fixture: within 2 ulp (the same summation order;
+    sqrt and divide correctly rounded on both sides)."""
+    _say("[golden] RMSNorm")
+    from vib3_amd import kernels as K
+    f, meta = load()
+    m = meta["rmsnorm"]
+    seed, stream, sigma = m["x"]
+    x = O.synth_normal_array(seed, stream, 0, m["n"], sigma, O.F32)
+    wseed, wstream, wsigma, woff = m["w"]
+    w = (O.synth_normal_array(wseed, wstream, 0, m["n"], wsigma, O.F32) + np.float32(woff)).astype(
+        np.float16)
+    out = torch.empty(m["n"], dtype=torch.float32, device="cuda")
+    K.rms_norm_f32(torch.from_numpy(x).cuda(), out, torch.from_numpy(w).cuda(), m["n"], m["eps"])
+    torch.cuda.synchronize()
+    ref = f["rmsnorm_out"]
+    assert np.all(np.abs(out.cpu().numpy() - ref) <= 2 * np.spacing(np.abs(ref)))
