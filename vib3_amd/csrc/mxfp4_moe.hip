@@ -63,6 +63,13 @@ __device__ __forceinline__ uint4 ld16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint2 ld8(const void* p) {
+  const u32x2_t v = *(const __attribute__((address_space(1))) u32x2_t*)p;
+  return make_uint2(v.x, v.y);
+}
+
 __device__ __forceinline__ uint8_t ld_u8(const uint8_t* p) {
   return *(const __attribute__((address_space(1))) uint8_t*)p;
 }
@@ -301,17 +308,24 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
 //
 // The work items above with the tokens' activations staged in LDS, so a wave can read long
 // pieces of few rows: a workgroup owns 64 weight rows (gate/up: 32 up + the same 32 gate rows;
-// down: 64 rows), one 16-row tile per wave, and walks k in steps of 1024. Per step each wave
-// loads 512 contiguous bytes of each of its 16 rows (lane (r, g) takes the 16-byte pieces
-// g, g + 4, ... of row r), the workgroup stages the 16 tokens' 1024 activations in LDS once, and
-// the wave runs 32 MFMAs against them. Loads of step s + 1 (weights into registers, activations
+// down: 64 rows), one 16-row tile per wave, and walks k in steps of kMx2K = 512. Per step each
+// wave loads 256 contiguous bytes of each of its 16 rows (lane (r, g) takes the 16-byte pieces
+// g, g + 4, ... of row r), the workgroup stages the 16 tokens' 512 activations in LDS once, and
+// the wave runs 16 MFMAs against them. The step size sets the LDS per workgroup (2 x 16.5 KB)
+// and so the waves per CU: 512 keeps four workgroups (16 waves) on a CU and measured 726 us
+// per c4 batch, against 803 us for steps of 1024 (66 KB, two workgroups) and 730 us for 256.
+// Loads of step s + 1 (weights into registers, activations
 // into the other LDS buffer) are issued before step s's matrix-core work.
-constexpr int kMx2K = 1024;                   // k per step
+#ifndef VIB3_MX2_K
+#define VIB3_MX2_K 512  // k per step (build-time tuning knob: 256, 512 or 1024)
+#endif
+constexpr int kMx2K = VIB3_MX2_K;             // k per step
+constexpr int kMx2P = kMx2K / 128;            // 16-byte pieces per lane per step
 constexpr int kMx2Pitch = kMx2K + 8;          // LDS row pitch (halves), against bank conflicts
 
 struct Mx2W {
-  uint4 w[8];     // 16 bytes of pieces g + 4j, j = 0..7, of this lane's row
-  uint4 sc[2];    // the row's 32 E8M0 scales of the step
+  uint4 w[kMx2P];       // 16 bytes of pieces g + 4j, j < kMx2P, of this lane's row
+  uint32_t sc[kMx2P];   // the row's E8M0 scales of the step: byte g of word j = piece g + 4j
 };
 
 template <bool GATEUP>
@@ -337,36 +351,43 @@ __global__ __launch_bounds__(256) void k_mx_gemm2(MxArgs a) {
   const uint8_t* base = (const uint8_t*)a.table[(size_t)e * 3 + seg];
   const uint8_t* code = base + (size_t)row * pkb + (size_t)g * 16;
   const uint8_t* scl = base + (size_t)M * pkb + (size_t)row * nsb;
-  // activation staging: thread t copies 64 halves (8 x 16 bytes) of token t / 16 of the block
+  // activation staging: thread t copies kMx2K / 16 halves of token t / 16 of the block
   const int st_tok = tid >> 4, st_part = tid & 15;
   const int tk = p0 + st_tok;
   const bool st_ok = tk < t_e;
   const uint16_t* xrow =
       GATEUP ? a.x + (size_t)a.ent_tok[o_e + (st_ok ? tk : p0)] * K
              : a.h + (size_t)(o_e + (st_ok ? tk : p0)) * K;
-  xrow += st_part * 64;
+  xrow += st_part * (kMx2K / 16);
 
   auto load_w = [&](Mx2W& w, int k0) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) w.w[j] = ld16(code + k0 / 2 + j * 64);
-    w.sc[0] = ld16(scl + k0 / 32);
-    w.sc[1] = ld16(scl + k0 / 32 + 16);
-  };
-  auto load_x = [&](uint4 (&v)[8], int k0) {
+    for (int j = 0; j < kMx2P; j++) w.w[j] = ld16(code + k0 / 2 + j * 64);
+    if constexpr (kMx2P >= 4) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) v[j] = ld16(xrow + k0 + j * 8);
+      for (int j = 0; j < kMx2P / 4; j++) {
+        const uint4 v = ld16(scl + k0 / 32 + 16 * j);
+        w.sc[4 * j] = v.x, w.sc[4 * j + 1] = v.y, w.sc[4 * j + 2] = v.z, w.sc[4 * j + 3] = v.w;
+      }
+    } else {
+      const uint2 v = ld8(scl + k0 / 32);
+      w.sc[0] = v.x, w.sc[1] = v.y;
+    }
   };
-  auto store_x = [&](const uint4 (&v)[8], int b) {
-    uint4* d = (uint4*)&xs[b][st_tok][st_part * 64];
+  auto load_x = [&](uint4 (&v)[kMx2P], int k0) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) d[j] = v[j];
+    for (int j = 0; j < kMx2P; j++) v[j] = ld16(xrow + k0 + j * 8);
+  };
+  auto store_x = [&](const uint4 (&v)[kMx2P], int b) {
+    uint4* d = (uint4*)&xs[b][st_tok][st_part * (kMx2K / 16)];
+#pragma unroll
+    for (int j = 0; j < kMx2P; j++) d[j] = v[j];
   };
   f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto compute = [&](const Mx2W& w, int b) {
-    const uint32_t scw[8] = {w.sc[0].x, w.sc[0].y, w.sc[0].z, w.sc[0].w,
-                             w.sc[1].x, w.sc[1].y, w.sc[1].z, w.sc[1].w};
+    const uint32_t* scw = w.sc;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = 0; j < kMx2P; j++) {
       // piece g + 4j covers k = 128 j + 32 g .. + 31 of the step: E8M0 byte 4j + g
       const float scale = e8m0_scale((uint8_t)(scw[j] >> (8 * g)));
       const uint32_t words[4] = {w.w[j].x, w.w[j].y, w.w[j].z, w.w[j].w};
@@ -388,7 +409,7 @@ __global__ __launch_bounds__(256) void k_mx_gemm2(MxArgs a) {
 
   const int nsteps = K / kMx2K;
   Mx2W W0, W1;
-  uint4 xv[8];
+  uint4 xv[kMx2P];
   load_w(W0, 0);
   load_x(xv, 0);
   store_x(xv, 0);
