@@ -307,19 +307,25 @@ __global__ __launch_bounds__(256) void k_mx_gemm(MxArgs a) {
 // ----------------------------------------------------------------------- matrix-core path, v2
 //
 // The work items above with the tokens' activations staged in LDS, so a wave can read long
-// pieces of few rows: a workgroup owns 64 weight rows (gate/up: 32 up + the same 32 gate rows;
-// down: 64 rows), one 16-row tile per wave, and walks k in steps of kMx2K = 512. Per step each
-// wave loads 256 contiguous bytes of each of its 16 rows (lane (r, g) takes the 16-byte pieces
-// g, g + 4, ... of row r), the workgroup stages the 16 tokens' 512 activations in LDS once, and
-// the wave runs 16 MFMAs against them. The step size sets the LDS per workgroup (2 x 16.5 KB)
-// and so the waves per CU: 512 keeps four workgroups (16 waves) on a CU and measured 726 us
-// per c4 batch, against 803 us for steps of 1024 (66 KB, two workgroups) and 730 us for 256.
+// pieces of few rows: a workgroup of kMx2W = 8 waves owns 128 weight rows (gate/up: 64 up + the
+// same 64 gate rows; down: 128 rows), one 16-row tile per wave, and walks k in steps of
+// kMx2K = 512. Per step each wave loads 256 contiguous bytes of each of its 16 rows (lane (r, g)
+// takes the 16-byte pieces g, g + 4, ... of row r), the workgroup stages the 16 tokens' 512
+// activations in LDS once, and the wave runs 16 MFMAs against them. Waves per CU decided the
+// rate: per c4 batch, 4-wave workgroups with steps of 1024 (66 KB LDS, 8 waves per CU) took
+// 803 us, with steps of 512 (33 KB, 16 waves) 726 us, 8-wave workgroups with steps of 512
+// (24 waves per CU) 704 us, and with steps of 256 722 us.
 // Loads of step s + 1 (weights into registers, activations
 // into the other LDS buffer) are issued before step s's matrix-core work.
 #ifndef VIB3_MX2_K
 #define VIB3_MX2_K 512  // k per step (build-time tuning knob: 256, 512 or 1024)
 #endif
 constexpr int kMx2K = VIB3_MX2_K;             // k per step
+#ifndef VIB3_MX2_WAVES
+#define VIB3_MX2_WAVES 8  // waves per workgroup sharing one activation stage (4 or 8)
+#endif
+constexpr int kMx2W = VIB3_MX2_WAVES;
+constexpr int kMx2H = kMx2W / 2;              // gate/up: waves per matrix
 constexpr int kMx2P = kMx2K / 128;            // 16-byte pieces per lane per step
 constexpr int kMx2Pitch = kMx2K + 8;          // LDS row pitch (halves), against bank conflicts
 
@@ -329,7 +335,7 @@ struct Mx2W {
 };
 
 template <bool GATEUP>
-__global__ __launch_bounds__(256) void k_mx_gemm2(MxArgs a) {
+__global__ __launch_bounds__(64 * kMx2W) void k_mx_gemm2(MxArgs a) {
   __shared__ uint16_t xs[2][kMxTokBlk][kMx2Pitch];
   const int item = (int)blockIdx.y;
   if (item >= *a.nitems) return;
@@ -342,23 +348,25 @@ __global__ __launch_bounds__(256) void k_mx_gemm2(MxArgs a) {
 
   const int K = GATEUP ? a.hidden : a.inter;
   const int M = GATEUP ? a.inter : a.hidden;
-  const int r0 = (int)blockIdx.x * (GATEUP ? 32 : 64);
+  const int r0 = (int)blockIdx.x * (GATEUP ? 16 * kMx2H : 16 * kMx2W);
   if (p0 >= t_e) return;  // (a guard; uniform)
   const size_t pkb = (size_t)K / 2, nsb = (size_t)K / 32;
   // this wave's tile: gate/up waves 0, 1 = up rows r0 + 16w, waves 2, 3 = gate rows r0 + 16(w-2)
-  const int seg = GATEUP ? (wave < 2 ? 0 : 1) : 2;
-  const int row = GATEUP ? r0 + (wave & 1) * 16 + rr : r0 + wave * 16 + rr;
+  const int seg = GATEUP ? (wave < kMx2H ? 0 : 1) : 2;
+  const int row = GATEUP ? r0 + (wave % kMx2H) * 16 + rr : r0 + wave * 16 + rr;
   const uint8_t* base = (const uint8_t*)a.table[(size_t)e * 3 + seg];
   const uint8_t* code = base + (size_t)row * pkb + (size_t)g * 16;
   const uint8_t* scl = base + (size_t)M * pkb + (size_t)row * nsb;
-  // activation staging: thread t copies kMx2K / 16 halves of token t / 16 of the block
-  const int st_tok = tid >> 4, st_part = tid & 15;
+  // activation staging: each of a token's kParts threads copies kXP x 16 bytes of its row
+  constexpr int kParts = 4 * kMx2W;            // staging threads per token
+  constexpr int kXP = kMx2K / (32 * kMx2W);    // 16-byte pieces per staging thread
+  const int st_tok = tid / kParts, st_part = tid % kParts;
   const int tk = p0 + st_tok;
   const bool st_ok = tk < t_e;
   const uint16_t* xrow =
       GATEUP ? a.x + (size_t)a.ent_tok[o_e + (st_ok ? tk : p0)] * K
              : a.h + (size_t)(o_e + (st_ok ? tk : p0)) * K;
-  xrow += st_part * (kMx2K / 16);
+  xrow += st_part * (kMx2K / kParts);
 
   auto load_w = [&](Mx2W& w, int k0) {
 #pragma unroll
@@ -374,14 +382,14 @@ __global__ __launch_bounds__(256) void k_mx_gemm2(MxArgs a) {
       w.sc[0] = v.x, w.sc[1] = v.y;
     }
   };
-  auto load_x = [&](uint4 (&v)[kMx2P], int k0) {
+  auto load_x = [&](uint4 (&v)[kXP], int k0) {
 #pragma unroll
-    for (int j = 0; j < kMx2P; j++) v[j] = ld16(xrow + k0 + j * 8);
+    for (int j = 0; j < kXP; j++) v[j] = ld16(xrow + k0 + j * 8);
   };
-  auto store_x = [&](const uint4 (&v)[kMx2P], int b) {
-    uint4* d = (uint4*)&xs[b][st_tok][st_part * (kMx2K / 16)];
+  auto store_x = [&](const uint4 (&v)[kXP], int b) {
+    uint4* d = (uint4*)&xs[b][st_tok][st_part * (kMx2K / kParts)];
 #pragma unroll
-    for (int j = 0; j < kMx2P; j++) d[j] = v[j];
+    for (int j = 0; j < kXP; j++) d[j] = v[j];
   };
   f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto compute = [&](const Mx2W& w, int b) {
@@ -409,7 +417,7 @@ __global__ __launch_bounds__(256) void k_mx_gemm2(MxArgs a) {
 
   const int nsteps = K / kMx2K;
   Mx2W W0, W1;
-  uint4 xv[kMx2P];
+  uint4 xv[kXP];
   load_w(W0, 0);
   load_x(xv, 0);
   store_x(xv, 0);
@@ -442,9 +450,9 @@ __global__ __launch_bounds__(256) void k_mx_gemm2(MxArgs a) {
     // the gate tiles (waves 2, 3) meet the up tiles (waves 0, 1) through LDS
     __syncthreads();
     f32x4_t* ex = (f32x4_t*)&xs[0][0][0];
-    if (wave >= 2) ex[(wave - 2) * kWave + lane] = acc;
+    if (wave >= kMx2H) ex[(wave - kMx2H) * kWave + lane] = acc;
     __syncthreads();
-    if (wave >= 2 || tok >= t_e) return;
+    if (wave >= kMx2H || tok >= t_e) return;
     const f32x4_t gt = ex[wave * kWave + lane];
     uint16_t hv[4];
 #pragma unroll
@@ -930,14 +938,16 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   // matrix-core path: activations staged in LDS when k is a multiple of 1024, otherwise
   // registers-only with k split over the waves (gate/up) or whole (down)
   if (B->hidden % kMx2K == 0)
-    hipLaunchKernelGGL((k_mx_gemm2<true>), dim3((unsigned)(B->inter / 32), items), dim3(256), 0,
+    hipLaunchKernelGGL((k_mx_gemm2<true>), dim3((unsigned)(B->inter / (16 * kMx2H)), items),
+                       dim3(64 * kMx2W), 0,
                        st, a);
   else
     hipLaunchKernelGGL((k_mx_gemm<true, 4>), dim3((unsigned)(B->inter / 32), items), dim3(256), 0,
                        st, a);
   mx_launch_rows<true>(a, B->hidden, st);
   if (B->inter % kMx2K == 0)
-    hipLaunchKernelGGL((k_mx_gemm2<false>), dim3((unsigned)(B->hidden / 64), items), dim3(256),
+    hipLaunchKernelGGL((k_mx_gemm2<false>), dim3((unsigned)(B->hidden / (16 * kMx2W)), items),
+                       dim3(64 * kMx2W),
                        0, st, a);
   else
     hipLaunchKernelGGL((k_mx_gemm<false, 1>), dim3((unsigned)(B->hidden / 256), items), dim3(256),
