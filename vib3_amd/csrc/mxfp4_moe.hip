@@ -51,8 +51,9 @@ struct MxArgs {
   const int* nitems;
   const int* ent_tok;         // [T*top_k] token of each entry (grouped by expert)
   const int* ent_slot;        // [T*top_k] t*top_k + j of each entry
-  const int* c_dix;           // [ncold] distinct index of each cold expert (row path)
-  const int* ncold;
+  const int* c_dix;           // [ncold] distinct index of each cold expert (row path): the
+  const int* ncold;           // ncold1 one-token experts first, then the two-token ones
+  const int* ncold1;
   uint16_t* h;                // [T*top_k][inter] f16, by entry
   uint16_t* d;                // [T*top_k][hidden] f16, by slot
   int hidden, inter;
@@ -622,9 +623,14 @@ __device__ __forceinline__ void mx_rows_segment(const MxArgs& a, int e, int o_e,
   }
 }
 
-template <bool GATEUP, int NCH>
-__global__ __launch_bounds__(256) void k_mx_rows(MxArgs a) {
-  const int ncold = *a.ncold;
+// One launch per token count: the one-token experts' segments hold half the activation
+// registers of the two-token ones, so their kernel keeps more waves per SIMD.
+template <bool GATEUP, int NCH, int NT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 && (GATEUP || NCH <= 2) ? 3 : 1)))
+void k_mx_rows(MxArgs a) {
+  const int n1 = *a.ncold1;
+  const int first = NT == 1 ? 0 : n1;
+  const int ncold = NT == 1 ? n1 : *a.ncold - n1;
   const int per = GATEUP ? a.inter : a.hidden / 4;  // items per expert
   const long n = (long)ncold * per;
   const int W = (int)gridDim.x * 4;
@@ -634,12 +640,9 @@ __global__ __launch_bounds__(256) void k_mx_rows(MxArgs a) {
     const int c = (int)(i / per);
     const int q0 = (int)(i - (long)c * per);
     const int q1 = (int)min((long)per, i1 - (long)c * per);
-    const int dix = a.c_dix[c];
-    const int e = a.d_expert[dix], o_e = a.d_off[dix], t_e = a.d_cnt[dix];
-    if (t_e == 1)
-      mx_rows_segment<GATEUP, NCH, 1>(a, e, o_e, q0, q1);
-    else
-      mx_rows_segment<GATEUP, NCH, 2>(a, e, o_e, q0, q1);
+    const int dix = a.c_dix[first + c];
+    const int e = a.d_expert[dix], o_e = a.d_off[dix];
+    mx_rows_segment<GATEUP, NCH, NT>(a, e, o_e, q0, q1);
     i = (long)c * per + q1;
   }
 }
@@ -669,8 +672,9 @@ struct MxGroupArgs {
   int* nitems;
   int* ent_tok;
   int* ent_slot;
-  int* c_dix;           // [ncold] distinct index of each expert of the row path
-  int* ncold;
+  int* c_dix;           // [ncold] distinct index of each expert of the row path (one-token
+  int* ncold;           // experts first)
+  int* ncold1;
   int top_k;
 };
 
@@ -678,6 +682,7 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int off[kMaxExperts];
   __shared__ int part[1024], dpart[1024], ipart[1024], cpart[1024];
+  static_assert(kMxColdMax == 2, "the row path lists one- and two-token experts");
   __shared__ uint16_t sid[kMxMaxPicks];
   const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
   for (int e = tid; e < a.E; e += nt) cnt[e] = 0;
@@ -692,51 +697,57 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
   const int span = (a.E + nt - 1) / nt;
   const int e0 = min(a.E, tid * span), e1 = min(a.E, e0 + span);
   // experts with 1..kMxColdMax entries go to the row path, the others to matrix-core items
-  int s = 0, ds = 0, is = 0, cs = 0;
+  // row-path experts are listed one-token ones first, then two-token ones (one launch each)
+  int s = 0, ds = 0, is = 0, c1 = 0, c2 = 0;
   for (int e = e0; e < e1; e++) {
     s += cnt[e];
     ds += cnt[e] > 0;
     is += cnt[e] > kMxColdMax ? mx_expert_items(cnt[e]) : 0;
-    cs += cnt[e] > 0 && cnt[e] <= kMxColdMax;
+    c1 += cnt[e] == 1;
+    c2 += cnt[e] == 2;
   }
-  // inclusive scans of the four counts over the workgroup: within each wave by lane shuffles,
+  // inclusive scans of the five counts over the workgroup: within each wave by lane shuffles,
   // then over the (at most 16) wave totals, with two barriers in all
-  int sc[4] = {s, ds, is, cs};
+  constexpr int kQ = 5;
+  int sc[kQ] = {s, ds, is, c1, c2};
   const int lane = tid & 63, wv = tid >> 6;
 #pragma unroll
   for (int st = 1; st < 64; st <<= 1) {
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
+    for (int q = 0; q < kQ; q++) {
       const int v = __shfl_up(sc[q], st, 64);
       if (lane >= st) sc[q] += v;
     }
   }
-  __shared__ int wtot[16][4];
+  __shared__ int wtot[16][kQ];
+  __shared__ int tot[kQ];
   if (lane == 63) {
 #pragma unroll
-    for (int q = 0; q < 4; q++) wtot[wv][q] = sc[q];
+    for (int q = 0; q < kQ; q++) wtot[wv][q] = sc[q];
   }
   __syncthreads();
-  if (tid < 4) {  // thread q scans the wave totals of count q
+  if (tid < kQ) {  // thread q scans the wave totals of count q
     int acc = 0;
     for (int w = 0; w < nt / 64; w++) {
       const int v = wtot[w][tid];
       wtot[w][tid] = acc;  // exclusive: what the waves before w hold
       acc += v;
     }
+    tot[tid] = acc;
   }
   __syncthreads();
 #pragma unroll
-  for (int q = 0; q < 4; q++) sc[q] += wtot[wv][q];
+  for (int q = 0; q < kQ; q++) sc[q] += wtot[wv][q];
   part[tid] = sc[0];
   dpart[tid] = sc[1];
   ipart[tid] = sc[2];
-  cpart[tid] = sc[3];
-  __syncthreads();  // the last thread's totals are read below
-  int run = part[tid] - s, drun = dpart[tid] - ds, irun = ipart[tid] - is, crun = cpart[tid] - cs;
+  cpart[tid] = tot[3] + tot[4];
+  int run = part[tid] - s, drun = dpart[tid] - ds, irun = ipart[tid] - is;
+  int c1run = sc[3] - c1, c2run = tot[3] + sc[4] - c2;
   for (int e = e0; e < e1; e++) {
     off[e] = run;
-    if (cnt[e] > 0 && cnt[e] <= kMxColdMax) a.c_dix[crun++] = drun;
+    if (cnt[e] == 1) a.c_dix[c1run++] = drun;
+    if (cnt[e] == 2) a.c_dix[c2run++] = drun;
     if (cnt[e] > 0) {
       a.d_expert[drun] = e;
       a.d_off[drun] = run;
@@ -757,7 +768,8 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
   if (tid == nt - 1) {
     *a.nd = dpart[nt - 1];
     *a.nitems = ipart[nt - 1];
-    *a.ncold = cpart[nt - 1];
+    *a.ncold = tot[3] + tot[4];
+    *a.ncold1 = tot[3];
   }
 
   __syncthreads();
@@ -840,15 +852,15 @@ static void mx_launch_rows(const MxArgs& a, int K, hipStream_t st) {
     hipLaunchKernelGGL(kernel, dim3((unsigned)g), dim3(256), 0, st, a);
   };
   switch (nch) {
-    case 1: launch(k_mx_rows<GATEUP, 1>); break;
-    case 2: launch(k_mx_rows<GATEUP, 2>); break;
-    case 3: launch(k_mx_rows<GATEUP, 3>); break;
-    default: launch(k_mx_rows<GATEUP, 4>); break;
+    case 1: launch(k_mx_rows<GATEUP, 1, 1>); launch(k_mx_rows<GATEUP, 1, 2>); break;
+    case 2: launch(k_mx_rows<GATEUP, 2, 1>); launch(k_mx_rows<GATEUP, 2, 2>); break;
+    case 3: launch(k_mx_rows<GATEUP, 3, 1>); launch(k_mx_rows<GATEUP, 3, 2>); break;
+    default: launch(k_mx_rows<GATEUP, 4, 1>); launch(k_mx_rows<GATEUP, 4, 2>); break;
   }
 }
 
 struct MxWs {
-  size_t d_expert, d_off, d_cnt, nd, it_d, it_p0, it_np, nitems, ent_tok, ent_slot, c_dix, ncold,
+  size_t d_expert, d_off, d_cnt, nd, it_d, it_p0, it_np, nitems, ent_tok, ent_slot, c_dix, ncold, ncold1,
       h, d, total;
 };
 
@@ -880,6 +892,7 @@ static MxWs mx_ws(const vib3_moe_mxfp4_batch* B) {
   w.ent_slot = take(sizeof(int) * n);
   w.c_dix = take(sizeof(int) * B->num_experts);
   w.ncold = take(sizeof(int));
+  w.ncold1 = take(sizeof(int));
   w.h = take(2 * n * B->inter);
   w.d = take(2 * n * B->hidden);
   w.total = o;
@@ -923,6 +936,7 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   ga.it_d = (int*)(ws + w.it_d); ga.it_p0 = (int*)(ws + w.it_p0); ga.it_np = (int*)(ws + w.it_np);
   ga.nitems = (int*)(ws + w.nitems);
   ga.c_dix = (int*)(ws + w.c_dix); ga.ncold = (int*)(ws + w.ncold);
+  ga.ncold1 = (int*)(ws + w.ncold1);
   ga.top_k = B->top_k;
   hipLaunchKernelGGL(k_mx_group, dim3(1), dim3(1024), 0, st, ga);
 
@@ -931,7 +945,7 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   a.d_expert = ga.d_expert; a.d_off = ga.d_off; a.d_cnt = ga.d_cnt; a.nd = ga.nd;
   a.it_d = ga.it_d; a.it_p0 = ga.it_p0; a.it_np = ga.it_np; a.nitems = ga.nitems;
   a.ent_tok = ga.ent_tok; a.ent_slot = ga.ent_slot;
-  a.c_dix = ga.c_dix; a.ncold = ga.ncold;
+  a.c_dix = ga.c_dix; a.ncold = ga.ncold; a.ncold1 = ga.ncold1;
   a.h = (uint16_t*)(ws + w.h); a.d = (uint16_t*)(ws + w.d);
   a.hidden = B->hidden; a.inter = B->inter;
   const unsigned items = (unsigned)mx_max_items(B);
