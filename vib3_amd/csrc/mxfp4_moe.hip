@@ -327,17 +327,23 @@ constexpr int kMx2K = VIB3_MX2_K;             // k per step
 #endif
 constexpr int kMx2W = VIB3_MX2_WAVES;
 constexpr int kMx2H = kMx2W / 2;              // gate/up: waves per matrix
-constexpr int kMx2P = kMx2K / 128;            // 16-byte pieces per lane per step
-constexpr int kMx2Pitch = kMx2K + 8;          // LDS row pitch (halves), against bank conflicts
+#ifndef VIB3_MX2_KD
+#define VIB3_MX2_KD 512  // k per step of the down phase (k = inter; 256 or 512)
+#endif
+constexpr int kMx2KD = VIB3_MX2_KD;
 
+template <int P>  // P = 16-byte pieces per lane per step
 struct Mx2W {
-  uint4 w[kMx2P];       // 16 bytes of pieces g + 4j, j < kMx2P, of this lane's row
-  uint32_t sc[kMx2P];   // the row's E8M0 scales of the step: byte g of word j = piece g + 4j
+  uint4 w[P];       // 16 bytes of pieces g + 4j, j < P, of this lane's row
+  uint32_t sc[P];   // the row's E8M0 scales of the step: byte g of word j = piece g + 4j
 };
 
-template <bool GATEUP>
+template <bool GATEUP, int KS>
 __global__ __launch_bounds__(64 * kMx2W) void k_mx_gemm2(MxArgs a) {
-  __shared__ uint16_t xs[2][kMxTokBlk][kMx2Pitch];
+  constexpr int kP = KS / 128;        // 16-byte pieces per lane per step
+  constexpr int kPitch = KS + 8;      // LDS row pitch (halves), against bank conflicts
+  static_assert(KS % (32 * kMx2W) == 0 && KS >= 256, "step width");
+  __shared__ uint16_t xs[2][kMxTokBlk][kPitch];
   const int item = (int)blockIdx.y;
   if (item >= *a.nitems) return;
   const int tid = (int)threadIdx.x, lane = lane_id();
@@ -360,21 +366,21 @@ __global__ __launch_bounds__(64 * kMx2W) void k_mx_gemm2(MxArgs a) {
   const uint8_t* scl = base + (size_t)M * pkb + (size_t)row * nsb;
   // activation staging: each of a token's kParts threads copies kXP x 16 bytes of its row
   constexpr int kParts = 4 * kMx2W;            // staging threads per token
-  constexpr int kXP = kMx2K / (32 * kMx2W);    // 16-byte pieces per staging thread
+  constexpr int kXP = KS / (32 * kMx2W);    // 16-byte pieces per staging thread
   const int st_tok = tid / kParts, st_part = tid % kParts;
   const int tk = p0 + st_tok;
   const bool st_ok = tk < t_e;
   const uint16_t* xrow =
       GATEUP ? a.x + (size_t)a.ent_tok[o_e + (st_ok ? tk : p0)] * K
              : a.h + (size_t)(o_e + (st_ok ? tk : p0)) * K;
-  xrow += st_part * (kMx2K / kParts);
+  xrow += st_part * (KS / kParts);
 
-  auto load_w = [&](Mx2W& w, int k0) {
+  auto load_w = [&](Mx2W<kP>& w, int k0) {
 #pragma unroll
-    for (int j = 0; j < kMx2P; j++) w.w[j] = ld16(code + k0 / 2 + j * 64);
-    if constexpr (kMx2P >= 4) {
+    for (int j = 0; j < kP; j++) w.w[j] = ld16(code + k0 / 2 + j * 64);
+    if constexpr (kP >= 4) {
 #pragma unroll
-      for (int j = 0; j < kMx2P / 4; j++) {
+      for (int j = 0; j < kP / 4; j++) {
         const uint4 v = ld16(scl + k0 / 32 + 16 * j);
         w.sc[4 * j] = v.x, w.sc[4 * j + 1] = v.y, w.sc[4 * j + 2] = v.z, w.sc[4 * j + 3] = v.w;
       }
@@ -388,15 +394,15 @@ __global__ __launch_bounds__(64 * kMx2W) void k_mx_gemm2(MxArgs a) {
     for (int j = 0; j < kXP; j++) v[j] = ld16(xrow + k0 + j * 8);
   };
   auto store_x = [&](const uint4 (&v)[kXP], int b) {
-    uint4* d = (uint4*)&xs[b][st_tok][st_part * (kMx2K / kParts)];
+    uint4* d = (uint4*)&xs[b][st_tok][st_part * (KS / kParts)];
 #pragma unroll
     for (int j = 0; j < kXP; j++) d[j] = v[j];
   };
   f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](const Mx2W& w, int b) {
+  auto compute = [&](const Mx2W<kP>& w, int b) {
     const uint32_t* scw = w.sc;
 #pragma unroll
-    for (int j = 0; j < kMx2P; j++) {
+    for (int j = 0; j < kP; j++) {
       // piece g + 4j covers k = 128 j + 32 g .. + 31 of the step: E8M0 byte 4j + g
       const float scale = e8m0_scale((uint8_t)(scw[j] >> (8 * g)));
       const uint32_t words[4] = {w.w[j].x, w.w[j].y, w.w[j].z, w.w[j].w};
@@ -416,8 +422,8 @@ __global__ __launch_bounds__(64 * kMx2W) void k_mx_gemm2(MxArgs a) {
     }
   };
 
-  const int nsteps = K / kMx2K;
-  Mx2W W0, W1;
+  const int nsteps = K / KS;
+  Mx2W<kP> W0, W1;
   uint4 xv[kXP];
   load_w(W0, 0);
   load_x(xv, 0);
@@ -427,8 +433,8 @@ __global__ __launch_bounds__(64 * kMx2W) void k_mx_gemm2(MxArgs a) {
     // step s from W0 / buffer 0, while step s + 1 loads into W1 / buffer 1
     const bool more1 = s + 1 < nsteps;
     if (more1) {  // activations first: waiting for them must not wait for these weights
-      load_x(xv, (s + 1) * kMx2K);
-      load_w(W1, (s + 1) * kMx2K);
+      load_x(xv, (s + 1) * KS);
+      load_w(W1, (s + 1) * KS);
     }
     compute(W0, 0);
     if (!more1) break;
@@ -436,8 +442,8 @@ __global__ __launch_bounds__(64 * kMx2W) void k_mx_gemm2(MxArgs a) {
     __syncthreads();
     const bool more2 = s + 2 < nsteps;
     if (more2) {
-      load_x(xv, (s + 2) * kMx2K);
-      load_w(W0, (s + 2) * kMx2K);
+      load_x(xv, (s + 2) * KS);
+      load_w(W0, (s + 2) * KS);
     }
     compute(W1, 1);
     if (!more2) break;
@@ -949,18 +955,18 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   a.h = (uint16_t*)(ws + w.h); a.d = (uint16_t*)(ws + w.d);
   a.hidden = B->hidden; a.inter = B->inter;
   const unsigned items = (unsigned)mx_max_items(B);
-  // matrix-core path: activations staged in LDS when k is a multiple of 1024, otherwise
+  // matrix-core path: activations staged in LDS when k is a multiple of the step, otherwise
   // registers-only with k split over the waves (gate/up) or whole (down)
   if (B->hidden % kMx2K == 0)
-    hipLaunchKernelGGL((k_mx_gemm2<true>), dim3((unsigned)(B->inter / (16 * kMx2H)), items),
+    hipLaunchKernelGGL((k_mx_gemm2<true, kMx2K>), dim3((unsigned)(B->inter / (16 * kMx2H)), items),
                        dim3(64 * kMx2W), 0,
                        st, a);
   else
     hipLaunchKernelGGL((k_mx_gemm<true, 4>), dim3((unsigned)(B->inter / 32), items), dim3(256), 0,
                        st, a);
   mx_launch_rows<true>(a, B->hidden, st);
-  if (B->inter % kMx2K == 0)
-    hipLaunchKernelGGL((k_mx_gemm2<false>), dim3((unsigned)(B->hidden / (16 * kMx2W)), items),
+  if (B->inter % kMx2KD == 0)
+    hipLaunchKernelGGL((k_mx_gemm2<false, kMx2KD>), dim3((unsigned)(B->hidden / (16 * kMx2W)), items),
                        dim3(64 * kMx2W),
                        0, st, a);
   else
