@@ -156,6 +156,10 @@ int vib3_launch_router_topk_ex(const void *hidden, int hidden_dtype, const void 
  * ---------------------------------------------------------------------------------------- */
 
 #define VIB3_MOE_F32_INTERMEDIATE 1 /* keep h and the down outputs in f32 (no f16 rounding) */
+/* Test only: the fused router's bounded wait looks for a tag that no workgroup publishes and
+ * gives up after 64 polls, so vib3_moe_int4_layer_status reports 1. Every kernel still exits
+ * normally; the routing of such a launch is meaningless. */
+#define VIB3_MOE_TEST_ROUTER_TIMEOUT 0x100
 
 typedef struct vib3_moe_int4_layer {
     /* activation: x[hidden] */
@@ -205,8 +209,16 @@ typedef struct vib3_moe_int4_layer {
 } vib3_moe_int4_layer;
 
 /* Workspace bytes for `layer`. Zero a new workspace once before its first launch
- * (vib3_hip_zero): the router publishes logits there under per-launch tags, and 0 is never a tag. */
+ * (vib3_hip_zero): the fused router publishes logits there under tags (0 is never a tag). The
+ * tag word also lives in the workspace and advances on the device at the end of every launch,
+ * so a launch captured in a HIP graph gets a fresh tag on every replay. One workspace serves
+ * one launch at a time: launches sharing a workspace must be ordered (one stream). */
 size_t vib3_moe_int4_workspace_bytes(const vib3_moe_int4_layer *layer);
+
+/* Status word of the layer's workspace: 1 when a launch's bounded router wait gave up since
+ * the last clear (its routing is then not trustworthy), else 0; negative on an argument error.
+ * Synchronises `stream` to read it; clear != 0 resets it to 0. No reference counterpart. */
+int vib3_moe_int4_layer_status(const vib3_moe_int4_layer *layer, int clear, void *stream);
 
 /* 1 when the layer computes the router logits and top-k inside its gate/up kernel (up to 512
  * experts), 0 when the router runs as launches of its own. */

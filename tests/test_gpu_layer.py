@@ -30,12 +30,30 @@ def rel_l2(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
+def margin_ok(keys, k):
+    """The k-th and (k+1)-th selection keys differ by more than 1e-3 (where ids must match)."""
+    s = np.sort(np.asarray(keys, dtype=np.float64))[::-1]
+    return k >= len(s) or s[k - 1] - s[k] > 1e-3
+
+
+def sigmoid_keys(x, w_host, bias_host, hidden, num_experts, k):
+    _, _, scores = O.router(x.float().cpu().numpy(), w_host, O.F32, num_experts, hidden, k, 1,
+                            1.0, True, bias_host)
+    return 1 / (1 + np.exp(-scores.astype(np.float64))) + bias_host
+
+
 def check_layer(layer, bank, x, router_w_host, w_dt, bias_host, mode, scaling, k, faithful=True,
                 tol=1e-3, normalize=True):
-    from vib3_amd.moe import BankShape  # noqa: F401
-    sh = bank.shape
     out = layer.launch(x).cpu().numpy()
     torch.cuda.synchronize()
+    return verify_layer(layer, bank, x, out, router_w_host, w_dt, bias_host, mode, scaling, k,
+                        faithful, tol, normalize)
+
+
+def verify_layer(layer, bank, x, out, router_w_host, w_dt, bias_host, mode, scaling, k,
+                 faithful=True, tol=1e-3, normalize=True):
+    """The layer's last outputs (out, layer.ids / layer.wts) against the oracle for x."""
+    sh = bank.shape
     ids = layer.ids.cpu().numpy().view(np.uint16)[:k]
     wts = layer.wts.cpu().numpy()[:k]
     xh = x.float().cpu().numpy()
@@ -46,8 +64,7 @@ def check_layer(layer, bank, x, router_w_host, w_dt, bias_host, mode, scaling, k
         keys = sig + (bias_host if bias_host is not None else 0)
     else:
         keys = r_scores.astype(np.float64)
-    s = np.sort(keys)[::-1]
-    if k < sh.num_experts and s[k - 1] - s[k] <= 1e-3:
+    if not margin_ok(keys, k):
         pytest.skip("selection margin below 1e-3 for this seed")
     assert ids.tolist() == r_ids.tolist()
     assert np.allclose(wts, r_wts, rtol=1e-5)
@@ -73,6 +90,73 @@ def kimi():
     w, b = moe.make_router(shape, 0, SEED, 0.01, 0.1)
     torch.cuda.synchronize()
     return moe, shape, bank, w, b
+
+
+def test_c2_graph_replay(kimi):
+    """The whole layer captured once in a HIP graph and replayed for several tokens (new x
+    copied in between, an eager launch on the same workspace in the middle): the router tag
+    advances on the device, so every replay routes from its own logits."""
+    moe, shape, bank, w, b = kimi
+    from vib3_amd._lib import ROUTER_SIGMOID
+    _say("case: c2 graph capture + replays")
+    layer = moe.MoeInt4Layer(bank, w, b, top_k=8, scoring_mode=ROUTER_SIGMOID,
+                             scaling_factor=2.827, normalize=True)
+    xbuf = moe.make_activation(shape.hidden, 20, SEED).clone()
+    side = torch.cuda.Stream()
+    layer.launch(xbuf)  # eager first call (host-side caches warm outside the capture)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        layer.launch(xbuf, stream=side)
+    torch.cuda.synchronize()
+    # tokens whose selection margin exceeds 1e-3 (there the ids must match bit for bit)
+    wh, bh = w.cpu().numpy(), b.cpu().numpy()
+    tokens = [t for t in range(21, 60)
+              if margin_ok(sigmoid_keys(moe.make_activation(shape.hidden, t, SEED), wh, bh,
+                                        shape.hidden, shape.num_experts, 8), 8)][:5]
+    assert len(tokens) == 5
+    seen = set()
+    for i, token in enumerate(tokens[:4]):
+        xt = moe.make_activation(shape.hidden, token, SEED)
+        xbuf.copy_(xt)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        out = layer.out.cpu().numpy()
+        _say(f"  replay {i} token {token}")
+        verify_layer(layer, bank, xbuf, out, w.cpu().numpy(), O.F32, b.cpu().numpy(), 1, 2.827, 8)
+        seen.add(tuple(layer.ids.cpu().numpy().tolist()))
+        if i == 1:  # an eager launch between replays shares the workspace and its tag word
+            check_layer(layer, bank, moe.make_activation(shape.hidden, tokens[4], SEED), wh,
+                        O.F32, bh, 1, 2.827, 8)
+    assert len(seen) > 1  # the tokens routed differently: stale routing would repeat ids
+    assert layer.status() == 0
+    del graph
+
+
+def test_router_wait_timeout_reported():
+    """A router wait that gives up (forced from the host: the kernels poll for a tag nobody
+    publishes, with a 64-poll limit) is reported by vib3_moe_int4_layer_status; every kernel
+    exits normally and the next ordinary launch is correct."""
+    from vib3_amd import moe
+    from vib3_amd._lib import DT_BF16, MOE_TEST_ROUTER_TIMEOUT, ROUTER_SIGMOID
+    _say("case: router wait timeout status")
+    shape = moe.BankShape(hidden=1024, inter=256, group_size=32, scale_dtype=DT_BF16,
+                          scale_sigma=0.03, num_experts=40, num_shared=1)
+    bank = moe.Int4ExpertBank(shape, layer=3, seed=SEED)
+    w, bias = moe.make_router(shape, 3, SEED, 0.05, 0.1)
+    layer = moe.MoeInt4Layer(bank, w, bias, top_k=6, scoring_mode=ROUTER_SIGMOID,
+                             scaling_factor=1.5, normalize=True)
+    x = moe.make_activation(shape.hidden, 4, SEED)
+    assert layer.status() == 0
+    layer.flags = MOE_TEST_ROUTER_TIMEOUT
+    layer.launch(x)
+    torch.cuda.synchronize()
+    assert layer.status(clear=True) == 1
+    assert layer.status() == 0
+    layer.flags = 0
+    check_layer(layer, bank, x, w.cpu().numpy(), O.F32, bias.cpu().numpy(), 1, 1.5, 6)
+    assert layer.status() == 0
 
 
 @pytest.mark.parametrize("token", [0, 1, 2])

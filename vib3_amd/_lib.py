@@ -16,6 +16,7 @@ LIB_PATH = os.environ.get("VIB3_LIB") or os.path.join(HERE, "libvib3_hip.so")
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 ROUTER_SOFTMAX, ROUTER_SIGMOID = 0, 1
 MOE_F32_INTERMEDIATE = 1
+MOE_TEST_ROUTER_TIMEOUT = 0x100
 
 ERRORS = {-1: "unsupported shape or dtype", -2: "bad count", -3: "bad pointer or alignment",
           -4: "workspace too small", -5: "unexpected .vib3 file or page layout",
@@ -82,6 +83,7 @@ SIGNATURES = {
     "vib3_moe_int4_workspace_bytes": (S, [C.POINTER(MoeInt4Layer)]),
     "vib3_launch_moe_int4_layer": (I, [C.POINTER(MoeInt4Layer), P]),
     "vib3_moe_int4_router_fused": (I, [C.POINTER(MoeInt4Layer)]),
+    "vib3_moe_int4_layer_status": (I, [C.POINTER(MoeInt4Layer), I, P]),
     "vib3_launch_moe_int4_layer_stage": (I, [C.POINTER(MoeInt4Layer), I, P]),
     "vib3_moe_mxfp4_workspace_bytes": (S, [C.POINTER(MoeMxfp4Batch)]),
     "vib3_launch_moe_mxfp4_batched": (I, [C.POINTER(MoeMxfp4Batch), P]),

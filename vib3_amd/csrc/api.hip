@@ -67,8 +67,8 @@ __global__ void k_zero(uint4* p16, size_t n16, uint8_t* tail, size_t ntail) {
   if (i < ntail) tail[i] = 0;
 }
 
-// Workspace of the fused layer: [scores[E] | ids[k] | wts[k] | router slots u64[E] | error |
-// h[nslots][inter] | xn f32[hidden] (with a norm) | shared weights f32[num_shared] (gated)].
+// Workspace of the fused layer: [scores[E] | ids[k] | wts[k] | router slots u64[E] |
+// status: error i32, router tag u32 | h[nslots][inter] | xn f32[hidden] (with a norm) | shared weights f32[num_shared] (gated)].
 struct LayerWs {
   size_t scores, ids, wts, slots, error, h, xn, shared_w, total;
 };
@@ -84,12 +84,12 @@ int router_mode(const vib3_moe_int4_layer* L) {
   return mode == 2 ? kRouteFused : mode == 1 ? kRouteScores : kRouteGiven;
 }
 
-// Tag of a launch's router slots: process-wide counter, never 0 (a zeroed workspace holds 0).
-uint32_t next_generation() {
+// Router tag of a stage-by-stage timing launch (vib3_launch_moe_int4_layer_stage): a
+// process-wide counter with bit 31 set, so it never equals 0 (a zeroed slot) nor a device tag
+// (next_tag keeps those below 2^31). Whole-layer launches take their tag on the device.
+uint32_t stage_generation() {
   static std::atomic<uint32_t> gen{0};
-  uint32_t g = gen.fetch_add(1, std::memory_order_relaxed) + 1;
-  if (g == 0) g = gen.fetch_add(1, std::memory_order_relaxed) + 1;
-  return g;
+  return 0x80000000u | (gen.fetch_add(1, std::memory_order_relaxed) & 0x7fffffffu);
 }
 
 LayerWs layer_ws(const vib3_moe_int4_layer* L) {
@@ -101,7 +101,7 @@ LayerWs layer_ws(const vib3_moe_int4_layer* L) {
   w.wts = round_up(w.ids + 2 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
   w.slots = round_up(w.wts + 4 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
   w.error = round_up(w.slots + 8 * (size_t)(L->num_experts > 0 ? L->num_experts : 0), 256);
-  w.h = round_up(w.error + 4, 256);
+  w.h = round_up(w.error + 8, 256);  // error word, then the router tag word at error + 4
   w.xn = round_up(w.h + hsz * (size_t)(nslots > 0 ? nslots : 0) * (size_t)(L->inter > 0 ? L->inter : 0), 256);
   w.shared_w = round_up(w.xn + (L->norm_weight ? 4 * (size_t)(L->hidden > 0 ? L->hidden : 0) : 0), 256);
   w.total = round_up(w.shared_w + (L->shared_gate ? 4 * (size_t)(L->num_shared > 0 ? L->num_shared : 0) : 0), 256);
@@ -347,7 +347,16 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
       route = router_mode(L);
       router.slots = (uint64_t*)(ws + w.slots);
       router.error = (int*)(ws + w.error);
-      router.gen = next_generation();
+      router.spin_limit = kRouterSpinLimit;
+      if (L->flags & VIB3_MOE_TEST_ROUTER_TIMEOUT) {  // no slot matches: the wait gives up
+        router.poll_xor = 0x40000000u;
+        router.spin_limit = 64;
+      }
+      // whole layer: the tag lives in the workspace and advances on the device (graph
+      // replays get a new tag each); one stage alone: a host tag (the down kernel that would
+      // advance the word may not run)
+      if (only < 0 && route == kRouteFused) router.gen_word = (uint32_t*)(ws + w.error + 4);
+      else router.gen = stage_generation();
       if (run(0) && route != kRouteFused) {
         int rc = launch_router_logits(router, st);
         if (rc) return rc;
@@ -391,11 +400,30 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
   d.out = L->out;
   d.residual = L->residual;
   d.shared_w = shared_w;
+  d.gen_word = router.gen_word;
   return run(2) ? launch_down(d, st) : 0;
 }
 
 int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
   return moe_int4_layer(L, stream, -1);
+}
+
+int vib3_moe_int4_layer_status(const vib3_moe_int4_layer* L, int clear, void* stream) {
+  if (!L || !L->workspace) return VIB3_ERR_BAD_POINTER;
+  const LayerWs w = layer_ws(L);
+  if (L->workspace_bytes < w.total) return VIB3_ERR_WORKSPACE;
+  int* dev = (int*)((char*)L->workspace + w.error);
+  int host = 0;
+  hipError_t e = hipMemcpyAsync(&host, dev, sizeof(int), hipMemcpyDeviceToHost, S(stream));
+  if (e == hipSuccess) e = hipStreamSynchronize(S(stream));
+  if (e != hipSuccess) return (int)e;
+  if (clear && host) {
+    const int rc = vib3_hip_zero(dev, sizeof(int), stream);
+    if (rc) return rc;
+    e = hipStreamSynchronize(S(stream));
+    if (e != hipSuccess) return (int)e;
+  }
+  return host ? 1 : 0;
 }
 
 int vib3_moe_int4_router_fused(const vib3_moe_int4_layer* L) {

@@ -269,6 +269,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // pipeline serves the router rows, which every routed row waits for, first. (Cutting rows
   // into halves to spread them evenly over the two workgroups of a CU measured slower.)
   const bool fused = PAGED && a.route == kRouteFused;
+  if (fused && a.router.gen_word) a.router.gen = next_tag(*a.router.gen_word);
   const int E = a.router.E, G = (int)gridDim.x;
   auto publish = [&](int e, float v) {
     if (threadIdx.x == 0) {
@@ -574,6 +575,7 @@ __global__ __launch_bounds__(WIDE ? 1024 : 640) void k_down_combine(DownArgs a) 
     if (k + 2 >= n) break;
     q1 = advance(q0);
   }
+  advance_router_tag(a.gen_word);
 }
 
 // ------------------------------------------------------------------------- k_down_rows
@@ -823,6 +825,7 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
   // loads, and the compiler then waits for all of them at the loop head
   const int r = R * g0 + grp;
   if (sub == 0 && r < a.M) a.out[r] = a.residual ? a.residual[r] + o : o;  // engine.rs:5302
+  advance_router_tag(a.gen_word);
   VIB3_TRACE_POINT(3);
 }
 

@@ -33,9 +33,25 @@ struct RouterArgs {
   float* out_wts;
   // logits published in the gate/up kernel (fused routing): tagged slots, see select.h
   uint64_t* slots;     // [E]
-  uint32_t gen;        // this launch's tag (never 0)
+  // Tag of this launch's slots (never 0). With gen_word set, the tag lives on the device:
+  // the gate/up kernel uses next_tag(*gen_word) and the layer's down kernel stores that value
+  // back, so every launch (also every replay of a captured graph) publishes under a new tag.
+  // Without gen_word, `gen` is the tag (stage-by-stage timing launches).
+  uint32_t gen;
+  uint32_t* gen_word;
+  uint32_t poll_xor;   // 0; nonzero only in the forced-timeout test (no slot ever matches)
+  int spin_limit;      // polls before the wait gives up
   int* error;          // set to 1 if a wait gave up
 };
+
+// Polls of the fused router's bounded wait before it gives up and records an error.
+constexpr int kRouterSpinLimit = 1 << 20;
+
+// Device tags are 31-bit and never 0; host-side stage tags set bit 31, so the two never meet.
+__host__ __device__ inline uint32_t next_tag(uint32_t g) {
+  const uint32_t n = (g + 1) & 0x7fffffffu;
+  return n ? n : 1u;
+}
 
 int launch_router_logits(const RouterArgs& a, hipStream_t s, KTime t = {});
 int launch_router_select(const RouterArgs& a, hipStream_t s, KTime t = {});
@@ -93,7 +109,14 @@ struct DownArgs {
   float* out;
   const float* residual;  // out = residual + sum, or null
   const float* shared_w;  // [nslots - top_k] weights of the shared experts, or null (1.0)
+  uint32_t* gen_word;     // router tag word advanced by block 0 (fused routing), or null
 };
+
+// The down kernel, the layer's last, advances the router tag for the next launch. It runs
+// after the gate/up kernel on the same stream, so no launch still reads the old value.
+__device__ inline void advance_router_tag(uint32_t* gen_word) {
+  if (gen_word && blockIdx.x == 0 && threadIdx.x == 0) *gen_word = next_tag(*gen_word);
+}
 
 struct GenericArgs {
   const void* x;

@@ -292,8 +292,8 @@ __device__ inline void select_topk_regs(const RouterArgs& a, const float* scores
 // expert: generation tag << 32 | f32 bits, written with a device-scope atomic store by the
 // workgroup that computed it), then select. Tags make the wait independent of any ordering
 // between different addresses, so no device-wide fence is needed. The wait is bounded: after
-// kRouterSpinLimit polls the wave records an error and selects from what it has.
-constexpr int kRouterSpinLimit = 1 << 20;
+// RouterArgs::spin_limit polls (kRouterSpinLimit normally) the wave records an error, which
+// the host reads with vib3_moe_int4_layer_status, and selects from what it has.
 
 template <int R>
 __device__ inline void select_topk_published(const RouterArgs& a, int* sel, float* selv,
@@ -307,11 +307,11 @@ __device__ inline void select_topk_published(const RouterArgs& a, int* sel, floa
     for (int r = 0; r < R; r++) {
       const int e = min(lane + r * kWave, a.E - 1);
       const uint64_t v = __hip_atomic_load(a.slots + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ok &= (uint32_t)(v >> 32) == a.gen;
+      ok &= (uint32_t)(v >> 32) == (a.gen ^ a.poll_xor);
       sc[r] = __uint_as_float((uint32_t)v);
     }
     if (__all(ok)) break;
-    if (it >= kRouterSpinLimit) {
+    if (it >= a.spin_limit) {
       if (lane == 0) a.error[0] = 1;
       break;
     }

@@ -219,6 +219,14 @@ class MoeInt4Layer:
             raise _lib.Vib3Error("vib3_launch_moe_int4_layer", rc)
         return self.out
 
+    def status(self, clear: bool = False, stream=None) -> int:
+        """1 when a launch's router wait gave up since the last clear, else 0 (synchronises)."""
+        st = (stream or torch.cuda.current_stream(self.bank.device)).cuda_stream
+        rc = _lib.load().vib3_moe_int4_layer_status(self._desc(None), int(clear), st)
+        if rc < 0:
+            raise _lib.Vib3Error("vib3_moe_int4_layer_status", rc)
+        return rc
+
 
 def make_router(shape: BankShape, layer: int, seed: int, sigma: float, bias_sigma: Optional[float],
                 dtype=torch.float32, device="cuda"):
