@@ -45,6 +45,7 @@ extern "C" {
 #define VIB3_ERR_WORKSPACE (-4)
 #define VIB3_ERR_FORMAT (-5) /* a .vib3 file or its page layout is not what the reader expects */
 #define VIB3_ERR_IO (-6)     /* a .vib3 file could not be opened or mapped */
+#define VIB3_ERR_NOT_RESIDENT (-7) /* a page of a page table has no device address yet */
 
 /* ------------------------------------------------------------------------------------------
  * Reference-compatible launchers: same names, argument order and meaning as cuda_ffi.rs.
@@ -78,9 +79,22 @@ int vib3_launch_silu_mul(const void *up_result, const void *gate_result, void *o
 int vib3_launch_weighted_accumulate_f32(void *output, const void *expert_output, float weight,
                                         int dim, void *stream);
 
-/* cuda_ffi.rs:212 (kernels.cu:2092): out_f32[i] += weight * expert_f32[i]. */
+/* cuda_ffi.rs:212 (kernels.cu:2092, called from kernels.rs:2051 with the same five
+ * arguments): out_f32[i] += weight * expert_f32[i]. */
 int vib3_launch_weighted_accumulate_f32_f32(void *output, const void *expert_output,
                                             float weight, int dim, void *stream);
+
+/* cuda_ffi.rs:194 (kernels.cu:788, :1108; kernels.rs:1959): f16 accumulator,
+ * out_f16[i] = f16(f32(out_f16[i]) + weight * f32(expert_f16[i])). */
+int vib3_launch_weighted_accumulate(void *output, const void *expert_output, float weight,
+                                    int dim, void *stream);
+
+/* cuda_ffi.rs:222: out_f32[i] += dev_weight[0] * f32(expert_f16[i]) with the weight read
+ * from device memory (no host sync for a router weight). The reference declares this entry
+ * point but kernels.cu does not define it; this library does, with the declared meaning. */
+int vib3_launch_weighted_accumulate_f32_dev_scalar(void *output, const void *expert_output,
+                                                   const void *dev_weight, int dim,
+                                                   void *stream);
 
 /* cuda_ffi.rs:369 (kernels.cu:665, :1477): scores[e] = sum_d h_f32[d] * W_f16[e][d]. */
 int vib3_launch_router_gemv_f32(const void *hidden_state, const void *router_weights,
@@ -310,13 +324,37 @@ int vib3_file_read_page(const vib3_file *file, uint32_t index, void *dst, size_t
  * segment there; any number here): for each experts[i] of `layer` and each of its segments
  * segments[0..2] (up, gate, down: {0, 1, 2} for routed experts, {14, 15, 16} for shared ones),
  * table[(i*3 + s)*max_pages + page_idx] = page_addr[catalog index of that page] (where the
- * caller put the page, 0 = not resident, which is an error). rows_per_page[s] receives the
- * segment's rows per page; pages must cover rows [p*rows_per_page, ...) in order (the
- * converter's layout, convert.rs:1852-1865). Host memory in, host memory out. */
+ * caller put the page). rows_per_page[s] receives the segment's rows per page. Pages must
+ * cover rows [p*rows_per_page, ...) in order, every page but the last full (the converter's
+ * layout, convert.rs:1852-1865), and reach rows_required[s] rows (NULL: the file's
+ * expert_hidden_dim for up/gate and hidden_dim for down): a truncated segment is
+ * VIB3_ERR_FORMAT, a page whose address is 0 VIB3_ERR_NOT_RESIDENT. Host memory in and out. */
 int vib3_build_page_table(const vib3_file *file, uint16_t layer, const uint16_t *experts,
                           int num_experts, const uint16_t segments[3],
                           const uint64_t *page_addr, uint64_t *table, int max_pages,
-                          int rows_per_page[3]);
+                          int rows_per_page[3], const int *rows_required);
+
+/* One entry of the query planner's plan, query_planner.rs:38-43 ResolvedPage{id, device_ptr,
+ * row_start, row_count} with its PageId (types.rs:199-205, repr(C)) spelled out. device_ptr 0:
+ * the page is not resident on the device (buffer_manager.rs:775 get_page would fetch it). */
+typedef struct vib3_resolved_page {
+    uint16_t layer, expert, segment, page_idx;
+    uint64_t device_ptr;
+    uint16_t row_start, row_count;
+} vib3_resolved_page;
+
+/* The same table from the planner's ResolvedPage lists (the pages of one layer, any order):
+ * the page of (experts[i], segments[s], page_idx) goes to table[(i*3 + s)*max_pages + page_idx],
+ * with the checks of vib3_build_page_table against rows_required[s] (NULL: unchecked). Pages
+ * with device_ptr 0 leave their entry 0; their indices in `pages` are written to
+ * missing[0..max_missing) in table order (expert, segment, page), *num_missing receives their number and the call
+ * returns VIB3_ERR_NOT_RESIDENT: the caller fetches them (get_page) and builds again. The
+ * layer must not be launched on such a table. Host memory in and out. */
+int vib3_build_page_table_resolved(const vib3_resolved_page *pages, size_t num_pages,
+                                   const uint16_t *experts, int num_experts,
+                                   const uint16_t segments[3], const int rows_required[3],
+                                   uint64_t *table, int max_pages, int rows_per_page[3],
+                                   uint32_t *missing, int max_missing, int *num_missing);
 
 /* ------------------------------------------------------------------------------------------
  * Utilities

@@ -260,6 +260,14 @@ void v3o_weighted_accumulate_f32(float *out, const uint16_t *expert_f16, float w
     for (size_t i = 0; i < n; i++) out[i] += w * v3o_f16_to_f32(expert_f16[i]);
 }
 
+/* kernels.rs:1959-1996 weighted_accumulate CPU branch: f16 accumulator,
+ * o = f16(f32(o) + w * f32(e)). */
+void v3o_weighted_accumulate_f16(uint16_t *out, const uint16_t *expert_f16, float w, size_t n)
+{
+    for (size_t i = 0; i < n; i++)
+        out[i] = v3o_f32_to_f16(v3o_f16_to_f32(out[i]) + w * v3o_f16_to_f32(expert_f16[i]));
+}
+
 /* ------------------------------------------------------------------ router */
 
 typedef struct {

@@ -10,6 +10,7 @@
  *   v3o_swiglu_int4_acc      <- src/compute/kernels.rs:2932-3054 (cpu_swiglu_int4)
  *   v3o_partial_swiglu_int4  <- src/compute/kernels.rs:162-203 (partial_swiglu, INT4 arm)
  *   v3o_weighted_accumulate_f32 <- src/compute/kernels.rs:2000-2036
+ *   v3o_weighted_accumulate_f16 <- src/compute/kernels.rs:1959-1996
  *   v3o_router               <- src/compute/kernels.rs:2307-2440 (run_router_with_scoring_and_bias)
  *   v3o_quantize_int4        <- src/compute/kernels.rs:3778-3831 (quantize_weights_to_int4)
  *   v3o_dequantize_int4      <- src/compute/kernels.rs:3866-3927 (dequantize_int4_to_f32)
@@ -76,6 +77,8 @@ void v3o_partial_swiglu_int4(const uint16_t *x_f16, const uint8_t *up_page,
 
 /* out[i] += w * f32(expert_f16[i]) */
 void v3o_weighted_accumulate_f32(float *out, const uint16_t *expert_f16, float w, size_t n);
+/* out_f16[i] = f16(f32(out_f16[i]) + w * f32(expert_f16[i])) */
+void v3o_weighted_accumulate_f16(uint16_t *out, const uint16_t *expert_f16, float w, size_t n);
 
 /* Router: scores[e] = sum_d x[d]*W[e][d] (sequential fp32), then
  * mode 0 (softmax): stable sort desc on scores, keep k, softmax over the k;

@@ -47,6 +47,7 @@ def _declare(L: C.CDLL) -> None:
         "v3o_swiglu_int4_acc": (None, [P, P, P, S, S, S, I, P, I]),
         "v3o_partial_swiglu_int4": (None, [P, P, P, P, S, S]),
         "v3o_weighted_accumulate_f32": (None, [P, P, F, S]),
+        "v3o_weighted_accumulate_f16": (None, [P, P, F, S]),
         "v3o_router": (I, [P, P, I, S, S, S, I, F, I, P, P, P, P, I]),
         "v3o_quantize_int4": (None, [P, S, S, S, P]),
         "v3o_dequantize_int4": (None, [P, S, S, S, I, P]),
@@ -145,6 +146,13 @@ def weighted_accumulate_f32(out: np.ndarray, expert_f16: np.ndarray, w: float) -
     assert out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
     e = np.ascontiguousarray(expert_f16, dtype=np.uint16)
     lib().v3o_weighted_accumulate_f32(_p(out), _p(e), float(w), out.size)
+
+
+def weighted_accumulate_f16(out: np.ndarray, expert_f16: np.ndarray, w: float) -> None:
+    """kernels.rs:1959 weighted_accumulate CPU branch: f16 accumulator bits, in place."""
+    assert out.dtype == np.uint16 and out.flags["C_CONTIGUOUS"]
+    e = np.ascontiguousarray(expert_f16, dtype=np.uint16)
+    lib().v3o_weighted_accumulate_f16(_p(out), _p(e), float(w), out.size)
 
 
 def router(x, w, w_dt, num_experts, hidden, top_k, mode, scaling=1.0, normalize=True,

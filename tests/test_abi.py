@@ -55,3 +55,20 @@ def test_code_object_targets_gfx950(tmp_path):
                           f"--input={fb}"], capture_output=True, text=True, check=True)
     targets = [t for t in out.stdout.split() if t.startswith("hip")]
     assert targets == ["hipv4-amdgcn-amd-amdhsa--gfx950"]
+
+
+def test_integration_recipe_builds_a_complete_library(tmp_path):
+    """The build.rs recipe in INTEGRATION.md lists every translation unit build.py compiles,
+    and a library linked from exactly that list has no undefined vib3_* / launch_* symbol."""
+    from vib3_amd import build
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    m = re.search(r"let src = \[([^\]]*)\];", doc)
+    assert m, "INTEGRATION.md has no `let src = [...]` line"
+    srcs = re.findall(r'"([^"]+)"', m.group(1))
+    assert srcs == build.SOURCES
+    lib = build.build(sources=srcs, out=str(tmp_path / "libvib3_recipe.so"),
+                      objdir=str(tmp_path / "obj"))
+    out = subprocess.run(["nm", "-D", "--undefined-only", lib], capture_output=True, text=True,
+                         check=True).stdout
+    bad = [ln for ln in out.split() if "vib3" in ln or "launch_" in ln]
+    assert bad == []

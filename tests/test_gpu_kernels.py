@@ -251,6 +251,19 @@ def test_silu_mul_and_weighted_accumulate():
            _stream())
     ref = ref + np.float32(-1.5) * e32
     assert np.array_equal(dacc.cpu().numpy(), ref.astype(np.float32))
+    # f16 accumulator (kernels.rs:1959) and the device-scalar weight (cuda_ffi.rs:222)
+    o16 = O.f16_bits(np.random.default_rng(5).normal(0, 2, n))
+    do16 = _dev(o16)
+    L.call("vib3_launch_weighted_accumulate", do16.data_ptr(), da.data_ptr(), 0.37, n, _stream())
+    ref16 = o16.copy()
+    O.weighted_accumulate_f16(ref16, a, 0.37)
+    assert np.array_equal(do16.cpu().numpy().view(np.uint16), ref16)
+    wdev = _dev(np.array([0.81], dtype=np.float32))
+    L.call("vib3_launch_weighted_accumulate_f32_dev_scalar", dacc.data_ptr(), da.data_ptr(),
+           wdev.data_ptr(), n, _stream())
+    ref = ref.astype(np.float32)
+    O.weighted_accumulate_f32(ref, a, 0.81)
+    assert np.array_equal(dacc.cpu().numpy(), ref)
 
 
 # ---------------------------------------------------------------- router

@@ -216,6 +216,46 @@ def test_c3_paged_equals_contiguous(kimi):
     del paged
 
 
+def test_c3_converter_pages_from_resolved_plan(kimi):
+    """The converter's Kimi INT4 pages (520-row gate/up pages, 1820-row down pages,
+    convert.rs:1853-1865) at shuffled pool offsets, with the layer's tables built from the
+    planner's ResolvedPage lists (vib3_build_page_table_resolved): the same bits as the
+    contiguous layout. A plan with a page not resident is refused before any launch."""
+    moe, shape, bank, w, b = kimi
+    from vib3_amd._lib import ROUTER_SIGMOID
+    from vib3_amd.vib3file import build_page_table_resolved
+    _say("case: converter pages 520/520/1820 from a resolved plan")
+    conv = moe.Int4ExpertBank(shape, layer=0, seed=SEED, layout="paged",
+                              tile_rows=(520, 520, 1820), pool_bytes=12 << 30)
+    rows = (shape.inter, shape.inter, shape.hidden)
+    plan = conv.resolved_pages()
+    table, rpp, missing = build_page_table_resolved(plan, list(range(shape.num_experts)),
+                                                    (0, 1, 2), conv.max_pages, rows)
+    assert rpp == [520, 520, 1820] and missing == [] and conv.max_pages == 4
+    shared_plan = conv.resolved_pages([shape.num_experts])
+    stable, srpp, smissing = build_page_table_resolved(shared_plan, [0xFFFF], (14, 15, 16),
+                                                       conv.max_pages, rows)
+    assert srpp == rpp and smissing == []
+    assert np.array_equal(table.view(np.int64), conv.routed_table.cpu().numpy().ravel())
+    assert np.array_equal(stable.view(np.int64), conv.shared_table.cpu().numpy().ravel())
+    conv.routed_table = torch.from_numpy(table.view(np.int64)).cuda()
+    conv.shared_table = torch.from_numpy(stable.view(np.int64)).cuda()
+    lc = moe.MoeInt4Layer(bank, w, b, top_k=8, scoring_mode=ROUTER_SIGMOID, scaling_factor=2.827)
+    lp = moe.MoeInt4Layer(conv, w, b, top_k=8, scoring_mode=ROUTER_SIGMOID, scaling_factor=2.827)
+    for token in (3, 11):
+        x = moe.make_activation(shape.hidden, token, SEED)
+        a = lc.launch(x).cpu().numpy()
+        p = lp.launch(x).cpu().numpy()
+        assert np.array_equal(a, p)
+    # one down page of expert 7 evicted: the builder lists it instead of giving a table
+    evicted = [(l, e, s, q, 0 if (e == 7 and s == 2 and q == 1) else ptr, r0, rc)
+               for (l, e, s, q, ptr, r0, rc) in plan]
+    _, _, missing = build_page_table_resolved(evicted, list(range(shape.num_experts)),
+                                              (0, 1, 2), conv.max_pages, rows)
+    assert [evicted[i][1:4] for i in missing] == [(7, 2, 1)]
+    del conv
+
+
 def test_c1_mixtral_layer():
     """c1: Mixtral-shape layer: router fp32 [8, 4096], softmax top-2, 8 INT4 experts
     (gate/up [14336, 4096], down [4096, 14336], g=128, fp16 scales), x fp16."""

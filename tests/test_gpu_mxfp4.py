@@ -86,7 +86,7 @@ def test_synth_mxfp4_page_device_matches_oracle():
 
 @pytest.mark.parametrize("hidden,inter,E,T,k", [(256, 256, 12, 5, 3), (512, 768, 9, 37, 4),
                                                  (256, 256, 3, 70, 2), (2560, 6144, 12, 5, 3),
-                                                 (6144, 2560, 6, 9, 2)])
+                                                 (6144, 2560, 6, 9, 2), (4096, 4096, 8, 6, 2)])
 def test_small_batches_match_oracle(hidden, inter, E, T, k):
     """Shapes with 1..70 tokens per expert (row path, several 16-token matrix-core blocks, a
     64-token chunk and a remainder), experts picked twice by one token, experts never picked,

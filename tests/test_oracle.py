@@ -68,6 +68,22 @@ def test_kat_weighted_accumulate():
     assert out.tolist() == [6.0, 12.0, 18.0, 24.0]
 
 
+def test_kat_weighted_accumulate_f16():
+    """integration_test.rs:420 on its own entry point (weighted_accumulate, kernels.rs:1959):
+    f16 accumulator [1, 2, 3, 4] + 0.5 * [10, 20, 30, 40] = [6, 12, 18, 24]; and the f16
+    rounding of every sum against numpy's f16 conversion of the exact f64 value."""
+    out = O.f16_bits([1, 2, 3, 4])
+    O.weighted_accumulate_f16(out, O.f16_bits([10, 20, 30, 40]), 0.5)
+    assert O.to_f32(out, O.F16).tolist() == [6.0, 12.0, 18.0, 24.0]
+    rng = np.random.default_rng(7)
+    o = O.f16_bits(rng.normal(0, 2, 4000))
+    e = O.f16_bits(rng.normal(0, 2, 4000))
+    ref = (O.to_f32(o, O.F16).astype(np.float32) +
+           np.float32(0.37) * O.to_f32(e, O.F16).astype(np.float32)).astype(np.float16)
+    O.weighted_accumulate_f16(o, e, 0.37)
+    assert np.array_equal(o, ref.view(np.uint16))
+
+
 def test_kat_run_router_softmax():
     """integration_test.rs:454 — 4 experts, top-2, softmax weights sum to 1; plus closed form."""
     hidden, E = 8, 4

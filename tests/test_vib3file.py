@@ -62,6 +62,13 @@ def test_page_table(model):
         gap[f.expert_pages(0, 5)[1].catalog_index] = 0
         with pytest.raises(Exception) as err:
             f.build_page_table(0, list(range(8)), (0, 1, 2), gap, 3)
+        assert getattr(err.value, "code", None) == -7
+        # segments must reach the rows the kernels read: the file's 256 / 1024 rows pass,
+        # one more row than the pages hold is a truncated segment
+        f.build_page_table(0, list(range(8)), (0, 1, 2), addr, 3, rows_required=(256, 256, 1024))
+        with pytest.raises(Exception) as err:
+            f.build_page_table(0, list(range(8)), (0, 1, 2), addr, 3,
+                               rows_required=(256, 257, 1024))
         assert getattr(err.value, "code", None) == -5
         with pytest.raises(Exception):
             f.build_page_table(0, [9], (0, 1, 2), addr, 3)
@@ -133,3 +140,70 @@ def test_lz4_pages(tmp_path):
             assert f.page_bytes(p.catalog_index).tobytes() == datas[p.page_idx]
         ratio = f.expert_pages(0, 0)[0].compressed_size / 1000
         assert ratio < 0.05
+
+
+def _plan(E, rows, rpp, layer=2, base=1 << 40, skip=()):
+    """Planner pages of E experts: segment s of `rows[s]` rows cut into rpp[s]-row pages, in a
+    shuffled order; (expert, segment, page) in `skip` are not resident (device_ptr 0)."""
+    pages = []
+    for e in range(E):
+        for s in range(3):
+            n = -(-rows[s] // rpp[s])
+            for p in range(n):
+                r = min(rpp[s], rows[s] - p * rpp[s])
+                ptr = 0 if (e, s, p) in skip else base + ((e * 3 + s) * 64 + p) * 4096
+                pages.append((layer, e, s, p, ptr, p * rpp[s], r))
+    rng = np.random.default_rng(5)
+    return [pages[i] for i in rng.permutation(len(pages))]
+
+
+def test_page_table_from_resolved_pages():
+    """query_planner.rs:38-43 ResolvedPage lists (the converter's 520 / 1820-row Kimi pages,
+    convert.rs:1853-1865) into the fused layer's table: every (expert, segment, page) lands at
+    its address whatever the plan's order; a subset of experts selects their rows."""
+    from vib3_amd.vib3file import build_page_table_resolved
+    rows, rpp = (2048, 2048, 7168), (520, 520, 1820)
+    pages = _plan(6, rows, rpp)
+    table, got_rpp, missing = build_page_table_resolved(pages, [4, 1], (0, 1, 2), 4, rows)
+    assert got_rpp == list(rpp) and missing == []
+    t = table.reshape(2, 3, 4)
+    for (layer, e, s, p, ptr, r0, rc) in pages:
+        if e in (4, 1):
+            assert t[[4, 1].index(e), s, p] == ptr
+    assert np.count_nonzero(t) == 2 * (4 + 4 + 4)
+
+
+def test_page_table_resolved_errors_and_missing():
+    from vib3_amd._lib import Vib3Error
+    from vib3_amd.vib3file import build_page_table_resolved
+    rows, rpp = (2048, 2048, 7168), (520, 520, 1820)
+    # non-resident pages: listed (plan indices, in table order), entries left 0
+    skip = {(1, 0, 2), (3, 2, 0)}
+    pages = _plan(4, rows, rpp, skip=skip)
+    table, _, missing = build_page_table_resolved(pages, [0, 1, 2, 3], (0, 1, 2), 4, rows)
+    assert [(pages[i][1], pages[i][2], pages[i][3]) for i in missing] == sorted(skip)
+    t = table.reshape(4, 3, 4)
+    assert t[1, 0, 2] == 0 and t[3, 2, 0] == 0 and t[1, 0, 1] != 0
+    # truncated segment: the last down page dropped
+    pages = [p for p in _plan(2, rows, rpp) if not (p[2] == 2 and p[3] == 3)]
+    with pytest.raises(Vib3Error) as e:
+        build_page_table_resolved(pages, [0, 1], (0, 1, 2), 4, rows)
+    assert e.value.code == -5
+    # a gap (page 1 of up missing) and a short page that is not the last
+    pages = [p for p in _plan(1, rows, rpp) if not (p[2] == 0 and p[3] == 1)]
+    with pytest.raises(Vib3Error):
+        build_page_table_resolved(pages, [0], (0, 1, 2), 4, rows)
+    pages = _plan(1, rows, rpp)
+    pages = [(a, b, c, d, ptr, r0, 100 if (c == 1 and d == 0) else rc)
+             for (a, b, c, d, ptr, r0, rc) in pages]
+    with pytest.raises(Vib3Error):
+        build_page_table_resolved(pages, [0], (0, 1, 2), 4, rows)
+    # an expert absent from the plan, too few table columns, two layers in one plan
+    with pytest.raises(Vib3Error):
+        build_page_table_resolved(_plan(2, rows, rpp), [0, 5], (0, 1, 2), 4, rows)
+    with pytest.raises(Vib3Error) as e:
+        build_page_table_resolved(_plan(2, rows, rpp), [0], (0, 1, 2), 3, rows)
+    assert e.value.code == -2
+    mixed = _plan(1, rows, rpp) + [(3, 0, 0, 9, 1, 0, 1)]
+    with pytest.raises(Vib3Error):
+        build_page_table_resolved(mixed, [0], (0, 1, 2), 4, rows)

@@ -20,7 +20,7 @@ MOE_TEST_ROUTER_TIMEOUT = 0x100
 
 ERRORS = {-1: "unsupported shape or dtype", -2: "bad count", -3: "bad pointer or alignment",
           -4: "workspace too small", -5: "unexpected .vib3 file or page layout",
-          -6: ".vib3 file cannot be opened"}
+          -6: ".vib3 file cannot be opened", -7: "a page is not resident"}
 
 
 class Vib3Error(RuntimeError):
@@ -50,6 +50,16 @@ class MoeInt4Layer(C.Structure):
     ]
 
 
+class ResolvedPage(C.Structure):
+    """vib3_resolved_page (include/vib3_hip.h): query_planner.rs:38-43 ResolvedPage."""
+
+    _fields_ = [
+        ("layer", C.c_uint16), ("expert", C.c_uint16), ("segment", C.c_uint16),
+        ("page_idx", C.c_uint16), ("device_ptr", C.c_uint64), ("row_start", C.c_uint16),
+        ("row_count", C.c_uint16),
+    ]
+
+
 class MoeMxfp4Batch(C.Structure):
     """vib3_moe_mxfp4_batch (include/vib3_hip.h)."""
 
@@ -70,6 +80,8 @@ SIGNATURES = {
     "vib3_launch_silu_mul": (I, [P, P, P, I, P]),
     "vib3_launch_weighted_accumulate_f32": (I, [P, P, F, I, P]),
     "vib3_launch_weighted_accumulate_f32_f32": (I, [P, P, F, I, P]),
+    "vib3_launch_weighted_accumulate": (I, [P, P, F, I, P]),
+    "vib3_launch_weighted_accumulate_f32_dev_scalar": (I, [P, P, P, I, P]),
     "vib3_launch_router_gemv_f32": (I, [P, P, P, I, I, P]),
     "vib3_launch_router_topk": (I, [P, P, P, P, P, P, I, I, I, I, F, P]),
     "vib3_launch_rms_norm_f32": (I, [P, P, P, I, F, P]),
@@ -100,7 +112,8 @@ SIGNATURES = {
     "vib3_file_expert_pages": (I, [P, C.c_uint16, C.c_uint16, P, I, P]),
     "vib3_file_page_data": (I, [P, C.c_uint32, P, P]),
     "vib3_file_read_page": (I, [P, C.c_uint32, P, S, P]),
-    "vib3_build_page_table": (I, [P, C.c_uint16, P, I, P, P, P, I, P]),
+    "vib3_build_page_table": (I, [P, C.c_uint16, P, I, P, P, P, I, P, P]),
+    "vib3_build_page_table_resolved": (I, [P, S, P, I, P, P, P, I, P, P, I, P]),
     "vib3_hip_version": (C.c_char_p, []),
 }
 

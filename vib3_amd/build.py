@@ -35,19 +35,22 @@ def _run(cmd, verbose):
         raise RuntimeError("hipcc failed: " + " ".join(cmd[-3:]))
 
 
-def build(verbose: bool = False, extra_flags=()) -> str:
+def build(verbose: bool = False, extra_flags=(), sources=None, out: str = LIB,
+          objdir: str = OBJ) -> str:
+    """Compile `sources` (default SOURCES) and link them into `out`; returns `out`."""
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    os.makedirs(OBJ, exist_ok=True)
-    objs = [os.path.join(OBJ, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    sources = list(SOURCES if sources is None else sources)
+    os.makedirs(objdir, exist_ok=True)
+    objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in sources]
     cmds = [[hipcc, *HIPCC_FLAGS, *extra_flags, "-c", "-o", o, os.path.join(CSRC, s)]
-            for s, o in zip(SOURCES, objs)]
+            for s, o in zip(sources, objs)]
     jobs = min(len(cmds), max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB + ".tmp", *objs],
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out + ".tmp", *objs],
          verbose)
-    os.replace(LIB + ".tmp", LIB)
-    return LIB
+    os.replace(out + ".tmp", out)
+    return out
 
 
 if __name__ == "__main__":

@@ -61,6 +61,20 @@ __global__ void k_weighted_acc(float* out, const void* e, int e_f32, float w, in
   out[i] = add_mul_rn(out[i], w, v);
 }
 
+__global__ void k_weighted_acc_f16(uint16_t* out, const uint16_t* e, const float* wdev, float w,
+                                   int n) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i >= n) return;
+  if (wdev) w = wdev[0];
+  out[i] = f32_to_f16_bits(add_mul_rn(f16_to_f32(out[i]), w, f16_to_f32(e[i])));
+}
+
+__global__ void k_weighted_acc_dev(float* out, const uint16_t* e, const float* wdev, int n) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i >= n) return;
+  out[i] = add_mul_rn(out[i], wdev[0], f16_to_f32(e[i]));
+}
+
 __global__ void k_zero(uint4* p16, size_t n16, uint8_t* tail, size_t ntail) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n16) p16[i] = make_uint4(0, 0, 0, 0);
@@ -168,6 +182,29 @@ int vib3_launch_weighted_accumulate_f32(void* output, const void* expert_output,
   if (dim == 0) return 0;
   hipLaunchKernelGGL(k_weighted_acc, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0,
                      S(stream), (float*)output, expert_output, 0, weight, dim);
+  VIB3_RETURN_LAUNCH();
+}
+
+int vib3_launch_weighted_accumulate(void* output, const void* expert_output, float weight,
+                                    int dim, void* stream) {
+  if (dim < 0) return VIB3_ERR_BAD_COUNT;
+  if (!output || !expert_output) return VIB3_ERR_BAD_POINTER;
+  if (dim == 0) return 0;
+  hipLaunchKernelGGL(k_weighted_acc_f16, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0,
+                     S(stream), (uint16_t*)output, (const uint16_t*)expert_output, nullptr,
+                     weight, dim);
+  VIB3_RETURN_LAUNCH();
+}
+
+int vib3_launch_weighted_accumulate_f32_dev_scalar(void* output, const void* expert_output,
+                                                   const void* dev_weight, int dim,
+                                                   void* stream) {
+  if (dim < 0) return VIB3_ERR_BAD_COUNT;
+  if (!output || !expert_output || !dev_weight) return VIB3_ERR_BAD_POINTER;
+  if (dim == 0) return 0;
+  hipLaunchKernelGGL(k_weighted_acc_dev, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0,
+                     S(stream), (float*)output, (const uint16_t*)expert_output,
+                     (const float*)dev_weight, dim);
   VIB3_RETURN_LAUNCH();
 }
 

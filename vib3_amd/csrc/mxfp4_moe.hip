@@ -845,23 +845,27 @@ __global__ __launch_bounds__(256) void k_mx_combine(const uint16_t* d, const flo
   }
 }
 
-// Row-path launch: K = the reduction length picks the chunks per lane (K <= 8192).
+// One row-path kernel at its resident grid, cached per instantiation and device (each
+// <GATEUP, NCH, NT> variant has its own register budget and therefore its own occupancy).
+template <bool GATEUP, int NCH, int NT>
+static void mx_launch_rows_one(const MxArgs& a, hipStream_t st) {
+  static int grid[64] = {0};
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  int& g = grid[dev & 63];
+  if (!g) g = resident_blocks(k_mx_rows<GATEUP, NCH, NT>, 256);
+  hipLaunchKernelGGL((k_mx_rows<GATEUP, NCH, NT>), dim3((unsigned)g), dim3(256), 0, st, a);
+}
+
+// Row-path launches (one-token and two-token experts): K = the reduction length picks the
+// chunks per lane (K <= 8192).
 template <bool GATEUP>
 static void mx_launch_rows(const MxArgs& a, int K, hipStream_t st) {
-  const int nch = (K / 32 + 63) / 64;
-  auto launch = [&](auto kernel) {
-    static int grid[64] = {0};
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    int& g = grid[dev & 63];
-    if (!g) g = resident_blocks(kernel, 256);
-    hipLaunchKernelGGL(kernel, dim3((unsigned)g), dim3(256), 0, st, a);
-  };
-  switch (nch) {
-    case 1: launch(k_mx_rows<GATEUP, 1, 1>); launch(k_mx_rows<GATEUP, 1, 2>); break;
-    case 2: launch(k_mx_rows<GATEUP, 2, 1>); launch(k_mx_rows<GATEUP, 2, 2>); break;
-    case 3: launch(k_mx_rows<GATEUP, 3, 1>); launch(k_mx_rows<GATEUP, 3, 2>); break;
-    default: launch(k_mx_rows<GATEUP, 4, 1>); launch(k_mx_rows<GATEUP, 4, 2>); break;
+  switch ((K / 32 + 63) / 64) {
+    case 1: mx_launch_rows_one<GATEUP, 1, 1>(a, st); mx_launch_rows_one<GATEUP, 1, 2>(a, st); break;
+    case 2: mx_launch_rows_one<GATEUP, 2, 1>(a, st); mx_launch_rows_one<GATEUP, 2, 2>(a, st); break;
+    case 3: mx_launch_rows_one<GATEUP, 3, 1>(a, st); mx_launch_rows_one<GATEUP, 3, 2>(a, st); break;
+    default: mx_launch_rows_one<GATEUP, 4, 1>(a, st); mx_launch_rows_one<GATEUP, 4, 2>(a, st); break;
   }
 }
 

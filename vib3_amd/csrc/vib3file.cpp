@@ -265,46 +265,130 @@ int vib3_file_read_page(const vib3_file* f, uint32_t index, void* dst, size_t ca
   return VIB3_ERR_UNSUPPORTED;  // zstd: no codec in this build
 }
 
+}  // extern "C"
+
+namespace {
+
+// One page of one (expert, segment) on its way into the table.
+struct TablePage {
+  uint32_t page_idx, row_start, row_count;
+  uint64_t addr;
+  uint32_t source;  // index in the caller's list (catalog index or resolved-page index)
+};
+
+// Writes table row (i, s) from the pages of one segment and checks that they are what the
+// kernels address: page p holds rows [p * rpp, ...), every page but the last holds rpp rows
+// (convert.rs:1852-1865), pages are distinct and gap-free, and together they cover
+// rows_required rows (a truncated segment would leave the kernels reading address 0).
+// Pages whose address is 0 are not resident: they are appended to `missing` and make the
+// call return VIB3_ERR_NOT_RESIDENT once every other check has passed.
+int fill_segment(std::vector<TablePage>& pages, int i, int s, int rows_required, int max_pages,
+                 uint64_t* table, int rpp[3], uint32_t* missing, int max_missing,
+                 int* n_missing) {
+  if (pages.empty()) return VIB3_ERR_FORMAT;
+  std::sort(pages.begin(), pages.end(),
+            [](const TablePage& a, const TablePage& b) { return a.page_idx < b.page_idx; });
+  int covered = 0;
+  for (size_t j = 0; j < pages.size(); j++) {
+    const TablePage& p = pages[j];
+    if (p.page_idx >= (uint32_t)max_pages) return VIB3_ERR_BAD_COUNT;
+    if (p.page_idx != j) return VIB3_ERR_FORMAT;  // a gap or the same page twice
+    if (rpp[s] == 0 && p.page_idx == 0) rpp[s] = (int)p.row_count;
+    if (rpp[s] == 0 || p.row_count == 0 || p.row_start != p.page_idx * (uint32_t)rpp[s] ||
+        p.row_count > (uint32_t)rpp[s])
+      return VIB3_ERR_FORMAT;
+    if (j + 1 < pages.size() && p.row_count != (uint32_t)rpp[s])
+      return VIB3_ERR_FORMAT;  // only the last page may be short
+    covered = (int)(p.row_start + p.row_count);
+    table[((size_t)i * 3 + s) * max_pages + p.page_idx] = p.addr;
+    if (!p.addr) {
+      if (*n_missing < max_missing && missing) missing[*n_missing] = p.source;
+      (*n_missing)++;
+    }
+  }
+  if (rows_required > 0 && covered < rows_required) return VIB3_ERR_FORMAT;
+  return 0;
+}
+
+// Rows each segment must cover: the caller's, else the file's dimensions (gate/up rows =
+// expert_hidden_dim, down rows = hidden_dim); 0 = unchecked (no file, no caller value).
+void required_rows(const vib3_file* f, const int* rows_required, int out[3]) {
+  for (int s = 0; s < 3; s++) {
+    out[s] = rows_required ? rows_required[s] : 0;
+    if (!rows_required && f)
+      out[s] = (int)(s == 2 ? f->info.hidden_dim : f->info.expert_hidden_dim);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
 int vib3_build_page_table(const vib3_file* f, uint16_t layer, const uint16_t* experts,
                           int num_experts, const uint16_t segments[3],
                           const uint64_t* page_addr, uint64_t* table, int max_pages,
-                          int rows_per_page[3]) {
+                          int rows_per_page[3], const int* rows_required) {
   if (!f || !experts || !segments || !page_addr || !table || !rows_per_page)
     return VIB3_ERR_BAD_POINTER;
   if (num_experts <= 0 || max_pages <= 0) return VIB3_ERR_BAD_COUNT;
   memset(table, 0, sizeof(uint64_t) * (size_t)num_experts * 3 * max_pages);
-  int rpp[3] = {0, 0, 0};
+  int rpp[3] = {0, 0, 0}, need[3];
+  required_rows(f, rows_required, need);
+  int n_missing = 0;
   for (int i = 0; i < num_experts; i++) {
     auto it = f->experts.find((uint32_t)layer << 16 | experts[i]);
     if (it == f->experts.end()) return VIB3_ERR_FORMAT;
     const ExpertRange r = it->second;
+    const uint64_t qend = std::min<uint64_t>((uint64_t)r.first + r.count, f->catalog.size());
     for (int s = 0; s < 3; s++) {
-      int pages = 0;
-      const uint64_t qend = std::min<uint64_t>((uint64_t)r.first + r.count, f->catalog.size());
+      std::vector<TablePage> pages;
       for (uint64_t q = r.first; q < qend; q++) {
         const vib3_page_entry& p = f->catalog[q];
-        if (p.segment != segments[s]) continue;
-        // the kernels address page p as rows [p * rows_per_page, ...): every page of a segment
-        // but the last holds the same number of rows, in page order (convert.rs:1852-1865); a
-        // short page elsewhere shows up as the next page's row_start
-        if (p.page_idx >= max_pages) return VIB3_ERR_BAD_COUNT;
-        if (rpp[s] == 0 && p.page_idx == 0) rpp[s] = p.row_count;
-        if (rpp[s] == 0 || p.row_start != (uint32_t)p.page_idx * (uint32_t)rpp[s] ||
-            p.row_count > rpp[s])
-          return VIB3_ERR_FORMAT;
-        uint64_t& slot = table[((size_t)i * 3 + s) * max_pages + p.page_idx];
-        if (slot) return VIB3_ERR_FORMAT;  // the same page twice
-        slot = page_addr[q];
-        if (!slot) return VIB3_ERR_FORMAT;  // not resident
-        pages++;
+        if (p.segment == segments[s])
+          pages.push_back({p.page_idx, p.row_start, p.row_count, page_addr[q], (uint32_t)q});
       }
-      if (pages == 0) return VIB3_ERR_FORMAT;
-      for (int p = 0; p < pages; p++)  // distinct pages, each below max_pages: no gap allowed
-        if (!table[((size_t)i * 3 + s) * max_pages + p]) return VIB3_ERR_FORMAT;
+      const int rc = fill_segment(pages, i, s, need[s], max_pages, table, rpp, nullptr, 0,
+                                  &n_missing);
+      if (rc) return rc;
+    }
+  }
+  if (n_missing) return VIB3_ERR_NOT_RESIDENT;  // a page of the table has no address
+  for (int s = 0; s < 3; s++) rows_per_page[s] = rpp[s];
+  return 0;
+}
+
+int vib3_build_page_table_resolved(const vib3_resolved_page* pages, size_t num_pages,
+                                   const uint16_t* experts, int num_experts,
+                                   const uint16_t segments[3], const int rows_required[3],
+                                   uint64_t* table, int max_pages, int rows_per_page[3],
+                                   uint32_t* missing, int max_missing, int* num_missing) {
+  if ((!pages && num_pages) || !experts || !segments || !table || !rows_per_page ||
+      !num_missing || (max_missing > 0 && !missing))
+    return VIB3_ERR_BAD_POINTER;
+  if (num_experts <= 0 || max_pages <= 0 || max_missing < 0) return VIB3_ERR_BAD_COUNT;
+  *num_missing = 0;
+  memset(table, 0, sizeof(uint64_t) * (size_t)num_experts * 3 * max_pages);
+  // (expert, segment) -> its pages, in one pass over the plan
+  std::unordered_map<uint32_t, std::vector<TablePage>> by_key;
+  for (size_t q = 0; q < num_pages; q++) {
+    const vib3_resolved_page& p = pages[q];
+    if (p.layer != pages[0].layer) return VIB3_ERR_FORMAT;  // one layer per table
+    by_key[(uint32_t)p.expert << 16 | p.segment].push_back(
+        {p.page_idx, p.row_start, p.row_count, p.device_ptr, (uint32_t)q});
+  }
+  int rpp[3] = {0, 0, 0}, need[3];
+  required_rows(nullptr, rows_required, need);
+  for (int i = 0; i < num_experts; i++) {
+    for (int s = 0; s < 3; s++) {
+      auto it = by_key.find((uint32_t)experts[i] << 16 | segments[s]);
+      if (it == by_key.end()) return VIB3_ERR_FORMAT;
+      const int rc = fill_segment(it->second, i, s, need[s], max_pages, table, rpp, missing,
+                                  max_missing, num_missing);
+      if (rc) return rc;
     }
   }
   for (int s = 0; s < 3; s++) rows_per_page[s] = rpp[s];
-  return 0;
+  return *num_missing ? VIB3_ERR_NOT_RESIDENT : 0;
 }
 
 }  // extern "C"

@@ -69,8 +69,9 @@ class Int4ExpertBank:
         n_all = shape.num_experts + shape.num_shared
         if layout == "contiguous":
             self.rows_per_page = [shape.seg_dims(s)[0] for s in range(3)]
-        elif layout == "paged":
-            self.rows_per_page = [tile_rows] * 3
+        elif layout == "paged":  # tile_rows: one row count for all segments, or three
+            self.rows_per_page = list(tile_rows) if isinstance(tile_rows, (tuple, list)) \
+                else [tile_rows] * 3
         else:
             raise ValueError(layout)
         self.pages_per_seg = [math.ceil(shape.seg_dims(s)[0] / self.rows_per_page[s])
@@ -136,6 +137,23 @@ class Int4ExpertBank:
                     segp.append(self.pool[off: off + n].cpu().numpy())
             out.append(segp)
         return out, list(self.rows_per_page)
+
+    def resolved_pages(self, experts: Optional[Sequence[int]] = None):
+        """The bank as the query planner's ResolvedPage list (query_planner.rs:38-43): one
+        (layer, expert, segment, page_idx, device_ptr, row_start, row_count) per page of the
+        given experts (default: every routed expert); shared expert s is expert 0xFFFF with
+        segments 14/15/16 (types.rs:203)."""
+        E = self.shape.num_experts
+        want = set(range(E) if experts is None else experts)
+        base = self.pool.data_ptr()
+        out = []
+        for e, s, p, r, off in self.tiles:
+            if e < E and e in want:
+                out.append((self.layer, e, s, p, base + off, p * self.rows_per_page[s], r))
+            elif e >= E and e in want:
+                out.append((self.layer, 0xFFFF, 14 + s, p, base + off,
+                            p * self.rows_per_page[s], r))
+        return out
 
     @property
     def nbytes(self) -> int:

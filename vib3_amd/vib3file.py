@@ -124,16 +124,18 @@ class Vib3File:
         return np.concatenate([self.page_bytes(e.catalog_index) for e in pages])
 
     def build_page_table(self, layer: int, experts: List[int], segments, page_addr: np.ndarray,
-                         max_pages: int):
-        """vib3_build_page_table: host u64[len(experts)][3][max_pages] and rows per page."""
+                         max_pages: int, rows_required=None):
+        """vib3_build_page_table: host u64[len(experts)][3][max_pages] and rows per page.
+        rows_required (3 ints): rows each segment must cover (None: the file's dimensions)."""
         table = np.zeros(len(experts) * 3 * max_pages, dtype=np.uint64)
         rpp = (C.c_int * 3)()
         ex = np.asarray(experts, dtype=np.uint16)
         seg = np.asarray(segments, dtype=np.uint16)
         pa = np.ascontiguousarray(page_addr, dtype=np.uint64)
+        req = (C.c_int * 3)(*rows_required) if rows_required is not None else None
         _check("vib3_build_page_table", self._lib.vib3_build_page_table(
             self._h, layer, ex.ctypes.data, len(experts), seg.ctypes.data, pa.ctypes.data,
-            table.ctypes.data, max_pages, rpp))
+            table.ctypes.data, max_pages, rpp, req))
         return table, list(rpp)
 
 
@@ -254,3 +256,28 @@ def load_moe_layer(f: Vib3File, layer: int, device="cuda", scale_dtype: int = _l
               shared_gate=gate_w[:hidden] if gate_w is not None else None)
     kw.update(layer_kwargs)
     return MoeInt4Layer(bank, router_w, None, **kw)
+
+
+def build_page_table_resolved(pages, experts: List[int], segments, max_pages: int,
+                              rows_required=None):
+    """vib3_build_page_table_resolved over planner pages, each (layer, expert, segment,
+    page_idx, device_ptr, row_start, row_count). Returns (table u64[len(experts)*3*max_pages],
+    rows_per_page, missing): missing lists the indices of non-resident pages (device_ptr 0),
+    in which case the table must not be launched."""
+    lib = _lib.load()
+    arr = (_lib.ResolvedPage * max(len(pages), 1))()
+    for i, p in enumerate(pages):
+        arr[i] = _lib.ResolvedPage(*p)
+    table = np.zeros(len(experts) * 3 * max_pages, dtype=np.uint64)
+    rpp = (C.c_int * 3)()
+    ex = np.asarray(experts, dtype=np.uint16)
+    seg = np.asarray(segments, dtype=np.uint16)
+    req = (C.c_int * 3)(*rows_required) if rows_required is not None else None
+    missing = np.zeros(max(len(pages), 1), dtype=np.uint32)
+    n = C.c_int()
+    rc = lib.vib3_build_page_table_resolved(arr, len(pages), ex.ctypes.data, len(experts),
+                                            seg.ctypes.data, req, table.ctypes.data, max_pages,
+                                            rpp, missing.ctypes.data, missing.size, C.byref(n))
+    if rc not in (0, -7):
+        raise _lib.Vib3Error("vib3_build_page_table_resolved", rc)
+    return table, list(rpp), missing[: n.value].tolist()
