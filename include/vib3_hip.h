@@ -231,8 +231,22 @@ size_t vib3_moe_int4_workspace_bytes(const vib3_moe_int4_layer *layer);
 
 /* Status word of the layer's workspace: 1 when a launch's bounded router wait gave up since
  * the last clear (its routing is then not trustworthy), else 0; negative on an argument error.
- * Synchronises `stream` to read it; clear != 0 resets it to 0. No reference counterpart. */
+ * Synchronises `stream` to read it; clear != 0 resets it to 0. With layer->workspace NULL it
+ * reads the status of vib3_launch_moe_int4_layer_noalloc calls on the current device.
+ * No reference counterpart. */
 int vib3_moe_int4_layer_status(const vib3_moe_int4_layer *layer, int clear, void *stream);
+
+/* vib3_launch_moe_int4_layer without a caller workspace and without any allocation: the
+ * layer's scratch is a fixed 256 KiB device array of the library (one per GPU, held until the
+ * process ends); layer->workspace / workspace_bytes are ignored. A shape whose workspace
+ * (vib3_moe_int4_workspace_bytes plus 4 KiB) exceeds 256 KiB returns VIB3_ERR_WORKSPACE
+ * (c2: ~45 KiB; c1: ~60 KiB). All calls on one GPU share that scratch: calls that overlap in
+ * time on one GPU (two streams, two threads) race and must not be issued; calls ordered on
+ * one stream, also under graph capture and replay, are safe. Same kernels and results as
+ * vib3_launch_moe_int4_layer. No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+int vib3_launch_moe_int4_layer_noalloc(const vib3_moe_int4_layer *layer, void *stream);
 
 /* 1 when the layer computes the router logits and top-k inside its gate/up kernel (up to 512
  * experts), 0 when the router runs as launches of its own. */

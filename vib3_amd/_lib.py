@@ -96,6 +96,7 @@ SIGNATURES = {
     "vib3_launch_moe_int4_layer": (I, [C.POINTER(MoeInt4Layer), P]),
     "vib3_moe_int4_router_fused": (I, [C.POINTER(MoeInt4Layer)]),
     "vib3_moe_int4_layer_status": (I, [C.POINTER(MoeInt4Layer), I, P]),
+    "vib3_launch_moe_int4_layer_noalloc": (I, [C.POINTER(MoeInt4Layer), P]),
     "vib3_launch_moe_int4_layer_stage": (I, [C.POINTER(MoeInt4Layer), I, P]),
     "vib3_moe_mxfp4_workspace_bytes": (S, [C.POINTER(MoeMxfp4Batch)]),
     "vib3_launch_moe_mxfp4_batched": (I, [C.POINTER(MoeMxfp4Batch), P]),

@@ -1,6 +1,7 @@
 // api.hip — the C ABI of libvib3_hip (include/vib3_hip.h): argument checks, workspace layout
-// and launch sequences. All entry points are asynchronous on the caller's stream, allocate
-// nothing and keep no mutable global state, so they are reentrant across streams.
+// and launch sequences. All entry points are asynchronous on the caller's stream and allocate
+// nothing. They keep no mutable global state, so they are reentrant across streams, except
+// vib3_launch_moe_int4_layer_noalloc, whose calls share one device scratch per GPU.
 #include <string.h>
 
 #include <atomic>
@@ -87,6 +88,30 @@ struct LayerWs {
   size_t scores, ids, wts, slots, error, h, xn, shared_w, total;
 };
 
+// The no-allocation entry point's device memory: the layer workspace of
+// vib3_launch_moe_int4_layer_noalloc, at most kNoAllocScratchBytes. Every GPU the library runs
+// on holds its own copy (zero when the code object loads, which is the state the router tags
+// need) until the process ends. In host code `scratch` is only a symbol handle: its device
+// address, per device, comes from hipGetSymbolAddress (noalloc_scratch).
+constexpr size_t kNoAllocScratchBytes = 256 * 1024;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// Device address of this device's `scratch`, looked up once per device (set-up of the first
+// call on that device), or null if the lookup failed.
+char* noalloc_scratch() {
+  static std::atomic<char*> ptrs[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  char* p = ptrs[dev].load(std::memory_order_acquire);
+  if (!p) {
+    void* addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr) return nullptr;
+    p = (char*)addr;
+    ptrs[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
 // Routing mode of a layer call (see RowsArgs::route).
 int router_mode(const vib3_moe_int4_layer* L) {
   if (!L->router_w || L->top_k <= 0) return kRouteGiven;
@@ -106,16 +131,30 @@ uint32_t stage_generation() {
   return 0x80000000u | (gen.fetch_add(1, std::memory_order_relaxed) & 0x7fffffffu);
 }
 
-LayerWs layer_ws(const vib3_moe_int4_layer* L) {
+// scratch = true: the layout of the no-allocation scratch, whose status words (error, tag)
+// and router slots sit at fixed offsets for every layer shape: calls with different shapes
+// reuse the same bytes, and a slot must only ever hold an older tag of the same tag word.
+LayerWs layer_ws(const vib3_moe_int4_layer* L, bool scratch = false) {
   LayerWs w{};
   const int nslots = L->top_k + L->num_shared;
   const size_t hsz = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? 4 : 2;
-  w.scores = 0;
-  w.ids = round_up(w.scores + 4 * (size_t)(L->num_experts > 0 ? L->num_experts : 0), 256);
+  const size_t E = (size_t)(L->num_experts > 0 ? L->num_experts : 0);
+  if (scratch) {
+    w.error = 0;
+    w.slots = 256;
+    w.scores = round_up(w.slots + 8 * (size_t)kMaxExpertsInKernel, 256);
+  } else {
+    w.scores = 0;
+  }
+  w.ids = round_up(w.scores + 4 * E, 256);
   w.wts = round_up(w.ids + 2 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
-  w.slots = round_up(w.wts + 4 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
-  w.error = round_up(w.slots + 8 * (size_t)(L->num_experts > 0 ? L->num_experts : 0), 256);
-  w.h = round_up(w.error + 8, 256);  // error word, then the router tag word at error + 4
+  size_t next = round_up(w.wts + 4 * (size_t)(L->top_k > 0 ? L->top_k : 0), 256);
+  if (!scratch) {
+    w.slots = next;
+    w.error = round_up(w.slots + 8 * E, 256);
+    next = round_up(w.error + 8, 256);  // error word, then the router tag word at error + 4
+  }
+  w.h = next;
   w.xn = round_up(w.h + hsz * (size_t)(nslots > 0 ? nslots : 0) * (size_t)(L->inter > 0 ? L->inter : 0), 256);
   w.shared_w = round_up(w.xn + (L->norm_weight ? 4 * (size_t)(L->hidden > 0 ? L->hidden : 0) : 0), 256);
   w.total = round_up(w.shared_w + (L->shared_gate ? 4 * (size_t)(L->num_shared > 0 ? L->num_shared : 0) : 0), 256);
@@ -315,7 +354,10 @@ size_t vib3_moe_int4_workspace_bytes(const vib3_moe_int4_layer* L) {
 
 // only < 0: the whole layer; only = 0 / 1 / 2: just the router / gate-up / down launches, which
 // read what the earlier stages of a previous call left in the workspace (stage timing).
-static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) {
+// scratch: the no-allocation entry point's device scratch (used instead of L->workspace,
+// in its fixed layout), or null.
+static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only,
+                          char* scratch = nullptr) {
   if (!L) return VIB3_ERR_BAD_POINTER;
   if (!valid_act_dt(L->x_dtype) || !valid_scale_dt(L->scale_dtype)) return VIB3_ERR_UNSUPPORTED;
   if (L->hidden <= 0 || L->inter <= 0 || L->group_size <= 0 || L->top_k < 0 ||
@@ -331,16 +373,16 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only) 
       (L->rows_per_page[1] + 0LL) * L->max_pages < L->inter ||
       (L->rows_per_page[2] + 0LL) * L->max_pages < L->hidden)
     return VIB3_ERR_BAD_COUNT;
-  if (!L->x || !L->out || !L->workspace || (L->top_k > 0 && !L->page_table) ||
-      (L->num_shared > 0 && !L->shared_page_table) || !aligned16(L->x) ||
-      !aligned16(L->workspace))
+  if (!L->x || !L->out || (!scratch && (!L->workspace || !aligned16(L->workspace))) ||
+      (L->top_k > 0 && !L->page_table) || (L->num_shared > 0 && !L->shared_page_table) ||
+      !aligned16(L->x))
     return VIB3_ERR_BAD_POINTER;
   if (L->norm_weight && L->x_dtype != VIB3_DT_F32) return VIB3_ERR_UNSUPPORTED;  // f32 stream
   if ((L->norm_weight || L->shared_gate) && L->hidden > 8192) return VIB3_ERR_UNSUPPORTED;
   if (L->shared_gate && L->num_shared <= 0) return VIB3_ERR_BAD_COUNT;
-  const LayerWs w = layer_ws(L);
-  if (L->workspace_bytes < w.total) return VIB3_ERR_WORKSPACE;
-  char* ws = (char*)L->workspace;
+  const LayerWs w = layer_ws(L, scratch != nullptr);
+  if (w.total > (scratch ? kNoAllocScratchBytes : L->workspace_bytes)) return VIB3_ERR_WORKSPACE;
+  char* ws = scratch ? scratch : (char*)L->workspace;
   hipStream_t st = S(stream);
   auto run = [&](int i) { return only < 0 || only == i; };
 
@@ -445,11 +487,20 @@ int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer* L, void* stream) {
   return moe_int4_layer(L, stream, -1);
 }
 
+int vib3_launch_moe_int4_layer_noalloc(const vib3_moe_int4_layer* L, void* stream) {
+  char* ws = noalloc_scratch();
+  if (!ws) return VIB3_ERR_BAD_POINTER;
+  return moe_int4_layer(L, stream, -1, ws);
+}
+
 int vib3_moe_int4_layer_status(const vib3_moe_int4_layer* L, int clear, void* stream) {
-  if (!L || !L->workspace) return VIB3_ERR_BAD_POINTER;
-  const LayerWs w = layer_ws(L);
-  if (L->workspace_bytes < w.total) return VIB3_ERR_WORKSPACE;
-  int* dev = (int*)((char*)L->workspace + w.error);
+  if (!L) return VIB3_ERR_BAD_POINTER;
+  // workspace NULL: the status of vib3_launch_moe_int4_layer_noalloc calls on this device
+  char* base = L->workspace ? (char*)L->workspace : noalloc_scratch();
+  if (!base) return VIB3_ERR_BAD_POINTER;
+  const LayerWs w = layer_ws(L, !L->workspace);
+  if (L->workspace && L->workspace_bytes < w.total) return VIB3_ERR_WORKSPACE;
+  int* dev = (int*)(base + w.error);
   int host = 0;
   hipError_t e = hipMemcpyAsync(&host, dev, sizeof(int), hipMemcpyDeviceToHost, S(stream));
   if (e == hipSuccess) e = hipStreamSynchronize(S(stream));
