@@ -259,6 +259,64 @@ int vib3_launch_moe_int4_layer(const vib3_moe_int4_layer *layer, void *stream);
 int vib3_launch_moe_int4_layer_stage(const vib3_moe_int4_layer *layer, int stage, void *stream);
 
 /* ------------------------------------------------------------------------------------------
+ * The reference's sync-free fused MoE over NVFP4 pages (kernels.cu:5650-5990): FP4 activation
+ * (split-half E2M1, E8M0 per 32) times up/gate pages -> SwiGLU -> FP4 h -> down pages ->
+ * layer_output += w * down, for up to 8 experts. Pages hold tiled split-half E2M1 data
+ * (16 rows x 64 columns per 512-byte tile, after vib3_launch_repack_weights_inplace and
+ * vib3_launch_repack_row_to_tiled) followed by [rows][k/32] 2-byte scales whose exponent byte
+ * (s >> 7 & 0xff, a bf16's) is the E8M0 block scale (kernels.cu:5404-5411). Sums are exact
+ * (f64) and rounded once to f32, so results do not depend on launch order. Shapes: k_in and
+ * m_mid multiples of 128, m_out of 16, k_mid == m_mid, k_in <= 32768 and
+ * num_experts * m_mid <= 32768 (VIB3_ERR_UNSUPPORTED otherwise). A slot whose id is
+ * >= num_experts_total or whose table entry is 0 contributes nothing.
+ * ---------------------------------------------------------------------------------------- */
+
+/* cuda_ffi.rs:625 (kernels.cu:3193-3266): f32 input[K] -> act_fp4[K/2] split-half E2M1
+ * (16-byte aligned) and act_scales[K/32] E8M0 = round(log2 amax) - 2 + 127 per 32 values. */
+int vib3_launch_quantize_activation_fp4(const void *input, void *act_fp4, void *act_scales,
+                                        int K, void *stream);
+/* cuda_ffi.rs:770 (kernels.cu:5252): the same. */
+int vib3_launch_quantize_activation_fp4_fast(const void *input, void *act_fp4,
+                                             void *act_scales, int K, void *stream);
+
+/* cuda_ffi.rs:1026 (kernels.cu:6507): allocate the fused MoE's intermediate buffer (FP4 h of 8
+ * experts) on the current device; call once before launches and before graph capture. The
+ * fused launches never allocate: without it they return VIB3_ERR_WORKSPACE. */
+int vib3_moe_prewarm_gpu_bufs(int m_mid, int k_mid);
+
+/* cuda_ffi.rs:809 (kernels.cu:5650): host arrays of device pointers per expert (data and
+ * scales of up, gate, down) and host routing weights; layer_output accumulated (+=). */
+int vib3_launch_moe_experts_fused(const void *act_fp4, const void *act_scales,
+                                  const void *const *up_weight_ptrs,
+                                  const void *const *up_scale_ptrs,
+                                  const void *const *gate_weight_ptrs,
+                                  const void *const *gate_scale_ptrs,
+                                  const void *const *down_weight_ptrs,
+                                  const void *const *down_scale_ptrs,
+                                  const float *expert_weights_host, int num_experts, int K_in,
+                                  int M_mid, int K_mid, int M_out, float *layer_output,
+                                  void *stream);
+
+/* cuda_ffi.rs:831 (kernels.cu:5868): the same from a device page table
+ * page_table[(layer * num_experts_total + id) * 3 + seg] (engine.rs:1236-1299; seg 0 up,
+ * 1 gate, 2 down; scales at page + K/2 * rows) and device ids / weights of num_active experts. */
+int vib3_launch_moe_experts_fused_gpu(const void *act_fp4, const void *act_scales,
+                                      const uint64_t *page_table, const uint16_t *expert_ids,
+                                      const float *expert_weights, int layer,
+                                      int num_experts_total, int num_active, int K_in, int M_mid,
+                                      int K_mid, int M_out, float *layer_output, void *stream);
+
+/* cuda_ffi.rs:662 (kernels.cu:4132-4183): sequential nibble order -> split-half, in place, per
+ * 16-byte block of the page's data (a partial last block is left as it is). */
+int vib3_launch_repack_weights_inplace(void *weight_data_ptr, long long weight_data_bytes,
+                                       void *stream);
+
+/* cuda_ffi.rs:718 (kernels.cu:4227-4262): row-major split-half [M][K/2] -> tiled, through
+ * temp_buf (M*K/2 bytes), then copied back. M % 16 == 0, K % 64 == 0. */
+int vib3_launch_repack_row_to_tiled(void *weight_data_ptr, void *temp_buf, int M, int K,
+                                    void *stream);
+
+/* ------------------------------------------------------------------------------------------
  * Batched decode over MXFP4 experts (no counterpart in cuda_ffi.rs): T tokens, top_k picks
  * each, grouped per expert and run as a grouped GEMM on the CDNA4 matrix cores.
  * Per token t: h = f16(silu(gate_e . x_t) * (up_e . x_t)), d_j = f16(down_e . h),

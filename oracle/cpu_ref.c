@@ -669,3 +669,172 @@ void v3o_synth_mxfp4_page(uint64_t seed, uint64_t stream, size_t k, size_t row_s
     for (size_t i = 0; i < rows * nb; i++)
         sc[i] = v3o_synth_e8m0(seed, stream * 2 + 1, row_start * nb + i);
 }
+
+/* ------------------------------------------------------------------ NVFP4 fused MoE
+ * The reference's sync-free fused path (cuda/src/kernels.cu:5357-5591 kernels, :5650 / :5868
+ * launchers) over split-half E2M1 data with block scales, restated element by element. */
+
+/* kernels.cu:2759-2768 compute_e8m0: round(log2(amax)) - 2 + 127, clamped to [0, 254];
+ * round(log2) evaluated exactly as floor(log2) + (mantissa > sqrt 2). */
+uint8_t v3o_fp4_e8m0_of_amax(float amax)
+{
+    if (!(amax > 0.0f)) return 0;
+    uint32_t b = f2u(amax);
+    int E = (int)(b >> 23);
+    if (E == 0) return 0;
+    int n = E - 127 + ((b & 0x7fffff) > 0x3504f3 ? 1 : 0);
+    int biased = n + 125;
+    return (uint8_t)(biased < 0 ? 0 : biased > 254 ? 254 : biased);
+}
+
+/* E2M1 code of v: round to nearest on {0, .5, 1, 1.5, 2, 3, 4, 6}, ties to the even code,
+ * saturating at 6, sign bit from v (cvt.rn.satfinite of __nv_fp4x4_e2m1, kernels.cu:3227). */
+uint8_t v3o_e2m1_rne(float v)
+{
+    uint8_t sign = (uint8_t)((f2u(v) >> 31) << 3);
+    float a = fabsf(v);
+    uint8_t c;
+    if (a <= 0.25f) c = 0;
+    else if (a < 0.75f) c = 1;
+    else if (a <= 1.25f) c = 2;
+    else if (a < 1.75f) c = 3;
+    else if (a <= 2.5f) c = 4;
+    else if (a < 3.5f) c = 5;
+    else if (a <= 5.0f) c = 6;
+    else c = 7;
+    return sign | c;
+}
+
+/* e^x: Cody-Waite reduction with a two-part ln2 and the degree-7 Taylor polynomial of e^r in
+ * Horner form, then ldexp (the GPU kernel's exp, operation for operation). */
+float v3o_exp_cw(float x)
+{
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -103.97208404541015625f) return 0.0f;
+    float n = rintf(x * 1.44269502162933349609375f);
+    float r = x - n * 0.693145751953125f;
+    r = r - n * 1.428606765330187045e-06f;
+    float p = 1.0f / 5040.0f;
+    p = p * r + 1.0f / 720.0f;
+    p = p * r + 1.0f / 120.0f;
+    p = p * r + 1.0f / 24.0f;
+    p = p * r + 1.0f / 6.0f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return ldexpf(p, (int)n);
+}
+
+static float e8m0_inv(uint8_t e) { return e == 0 ? INFINITY : u2f((uint32_t)(254 - e) << 23); }
+
+/* kernels.cu:3193-3240 vib3_quantize_activation_fp4_kernel: per 32 values, e = E8M0 of the
+ * absolute maximum, inv = 1 / 2^(e-127) (0 when the group is all zero), code = E2M1(v * inv);
+ * split-half: byte j of the group = code(v[j]) | code(v[j+16]) << 4. */
+void v3o_fp4_quantize_act(const float *x, size_t k, uint8_t *codes, uint8_t *scales)
+{
+    size_t groups = (k + 31) / 32;
+    for (size_t g = 0; g < groups; g++) {
+        float v[32], amax = 0.0f;
+        for (int i = 0; i < 32; i++) {
+            v[i] = g * 32 + i < k ? x[g * 32 + i] : 0.0f;
+            amax = fmaxf(amax, fabsf(v[i]));
+        }
+        uint8_t e = v3o_fp4_e8m0_of_amax(amax);
+        float inv = amax == 0.0f ? 0.0f : e8m0_inv(e);
+        for (int j = 0; j < 16; j++)
+            if (g * 32 + j < k)
+                codes[g * 16 + j] = (uint8_t)(v3o_e2m1_rne(v[j] * inv) |
+                                              (v3o_e2m1_rne(v[j + 16] * inv) << 4));
+        scales[g] = e;
+    }
+}
+
+/* Code of element k of a split-half vector (byte k/32*16 + k%16, high nibble for k%32 >= 16). */
+static uint8_t split_code(const uint8_t *codes, size_t k)
+{
+    uint8_t b = codes[(k / 32) * 16 + (k % 16)];
+    return (k % 32) < 16 ? (b & 15) : (b >> 4);
+}
+
+/* Code of W[row][k] in the tiled split-half layout (kernels.cu:4185-4197). */
+static uint8_t tiled_code(const uint8_t *data, size_t row, size_t k, size_t K)
+{
+    size_t nkt = K / 64, t = k / 64, grp = (k % 64) / 32, j = k % 32;
+    uint8_t b = data[((row / 16) * nkt + t) * 512 + (row % 16) * 32 + grp * 16 + (j % 16)];
+    return j < 16 ? (b & 15) : (b >> 4);
+}
+
+/* out[r] = f32( sum_k e2m1(W[r][k]) 2^(ew(r,k/32)-127) * e2m1(a[k]) 2^(ea(k/32)-127) ), with
+ * ew the exponent byte of the row's bf16 scale (scale >> 7 & 0xff, kernels.cu:5404-5411): the
+ * exact value (f64, exact for scale spreads below 2^33) rounded once to f32. */
+void v3o_nvfp4_matvec(const uint8_t *act_codes, const uint8_t *act_scales, const uint8_t *data,
+                      const uint16_t *scales, size_t m, size_t k, float *out)
+{
+    size_t G = k / 32;
+    for (size_t r = 0; r < m; r++) {
+        double acc = 0.0;
+        for (size_t g = 0; g < G; g++) {
+            double s = 0.0;
+            for (size_t j = 0; j < 32; j++) {
+                size_t kk = g * 32 + j;
+                s += (double)v3o_e2m1(tiled_code(data, r, kk, k)) *
+                     (double)v3o_e2m1(split_code(act_codes, kk));
+            }
+            int ew = (scales[r * G + g] >> 7) & 0xff;
+            acc += s * ldexp(1.0, ew + (int)act_scales[g] - 254);
+        }
+        out[r] = (float)acc;
+    }
+}
+
+/* kernels.cu:5650 / :5868: for each active expert e (pages: up, gate, down tiled data and their
+ * scale arrays): u = up.a, g = gate.a (f32), h = (g * sigmoid(g)) * u with sigmoid = 1 / (1 +
+ * e^-g) (:5485-5487), h quantized like the activation (:5451-5517), d = down.h, then
+ * out[r] = out[r] + w_e * d[r] in expert order. */
+void v3o_moe_experts_fused(const uint8_t *act_codes, const uint8_t *act_scales,
+                           const uint8_t *const *data, const uint16_t *const *scales,
+                           const float *weights, size_t n, size_t k_in, size_t m_mid,
+                           size_t m_out, float *out)
+{
+    float *u = (float *)malloc(sizeof(float) * m_mid);
+    float *gt = (float *)malloc(sizeof(float) * m_mid);
+    float *h = (float *)malloc(sizeof(float) * m_mid);
+    uint8_t *hc = (uint8_t *)malloc(m_mid / 2 + 16);
+    uint8_t *hs = (uint8_t *)malloc(m_mid / 32 + 1);
+    float *d = (float *)malloc(sizeof(float) * m_out);
+    for (size_t e = 0; e < n; e++) {
+        v3o_nvfp4_matvec(act_codes, act_scales, data[e * 3 + 0], scales[e * 3 + 0], m_mid, k_in, u);
+        v3o_nvfp4_matvec(act_codes, act_scales, data[e * 3 + 1], scales[e * 3 + 1], m_mid, k_in, gt);
+        for (size_t i = 0; i < m_mid; i++) {
+            float sig = 1.0f / (1.0f + v3o_exp_cw(-gt[i]));
+            h[i] = (gt[i] * sig) * u[i];
+        }
+        v3o_fp4_quantize_act(h, m_mid, hc, hs);
+        v3o_nvfp4_matvec(hc, hs, data[e * 3 + 2], scales[e * 3 + 2], m_out, m_mid, d);
+        for (size_t r = 0; r < m_out; r++) out[r] = out[r] + weights[e] * d[r];
+    }
+    free(u); free(gt); free(h); free(hc); free(hs); free(d);
+}
+
+/* kernels.cu:4132-4160: sequential -> split-half per 16-byte block (a partial block is left). */
+void v3o_fp4_split_half(uint8_t *data, size_t nbytes)
+{
+    for (size_t b = 0; b + 16 <= nbytes; b += 16) {
+        uint8_t t[16];
+        memcpy(t, data + b, 16);
+        for (int j = 0; j < 8; j++) {
+            data[b + 2 * j] = (uint8_t)((t[j] & 0x0f) | ((t[j + 8] & 0x0f) << 4));
+            data[b + 2 * j + 1] = (uint8_t)((t[j] >> 4) | (t[j + 8] & 0xf0));
+        }
+    }
+}
+
+/* kernels.cu:4190-4225: row-major [m][k/2] -> tiles of 16 rows x 32 bytes. */
+void v3o_fp4_to_tiled(const uint8_t *src, uint8_t *dst, size_t m, size_t k)
+{
+    size_t pk = k / 2, nkt = pk / 32;
+    for (size_t row = 0; row < (m / 16) * 16; row++)
+        for (size_t t = 0; t < nkt; t++)
+            memcpy(dst + ((row / 16) * nkt + t) * 512 + (row % 16) * 32, src + row * pk + t * 32, 32);
+}

@@ -21,6 +21,10 @@
  *   v3o_residual_add_f32     <- cuda/src/kernels.cu:817 (vib3_residual_add_f32_f32_kernel)
  *   v3o_linear_row_f16       <- src/compute/kernels.rs:3630-3640 (linear_projection_f32_to_f32)
  *   v3o_mxfp4_*              <- cuda/src/kernels.cu:438-441 (E2M1 table), :2770-2777 (E8M0)
+ *   v3o_fp4_quantize_act     <- cuda/src/kernels.cu:3193-3240 (+ compute_e8m0 :2759-2768)
+ *   v3o_nvfp4_matvec         <- cuda/src/kernels.cu:5357-5449 (tiled split-half MMA GEMV)
+ *   v3o_moe_experts_fused    <- cuda/src/kernels.cu:5650-5834, :5868-5990 (fused NVFP4 MoE)
+ *   v3o_fp4_split_half / v3o_fp4_to_tiled <- cuda/src/kernels.cu:4132-4160, :4190-4225
  *   v3o_synth_*              synthetic-data generator spec shared with vib3_amd/csrc/synth.hip
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library,
@@ -146,6 +150,23 @@ void v3o_matmul_mxfp4_acc(const float *x, const uint8_t *codes, const uint8_t *s
 void v3o_moe_mxfp4_batched(const float *x, size_t tokens, size_t hidden, size_t inter,
                            const uint8_t *const *pages, size_t num_experts, const uint16_t *ids,
                            const float *weights, size_t top_k, uint16_t *out, int nthreads);
+
+/* ---- NVFP4 fused MoE (split-half E2M1, tiled weights, E8M0 = bf16 scale >> 7) ---- */
+uint8_t v3o_fp4_e8m0_of_amax(float amax);
+uint8_t v3o_e2m1_rne(float v);
+float v3o_exp_cw(float x);
+/* x[k] f32 -> codes[ceil(k/32) * 16] split-half, scales[ceil(k/32)] E8M0 */
+void v3o_fp4_quantize_act(const float *x, size_t k, uint8_t *codes, uint8_t *scales);
+/* out[m] = f32(exact sum over k of W[r][k] * a[k]); data tiled, scales [m][k/32] 2-byte */
+void v3o_nvfp4_matvec(const uint8_t *act_codes, const uint8_t *act_scales, const uint8_t *data,
+                      const uint16_t *scales, size_t m, size_t k, float *out);
+/* data[e*3 + {0 up, 1 gate, 2 down}], scales likewise; out[m_out] accumulated in place */
+void v3o_moe_experts_fused(const uint8_t *act_codes, const uint8_t *act_scales,
+                           const uint8_t *const *data, const uint16_t *const *scales,
+                           const float *weights, size_t n, size_t k_in, size_t m_mid,
+                           size_t m_out, float *out);
+void v3o_fp4_split_half(uint8_t *data, size_t nbytes);
+void v3o_fp4_to_tiled(const uint8_t *src, uint8_t *dst, size_t m, size_t k);
 
 /* ---- synthetic data generator (counter-based, identical spec in csrc/synth.hip) ---- */
 uint64_t v3o_synth_hash(uint64_t seed, uint64_t stream, uint64_t ctr);

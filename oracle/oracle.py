@@ -48,6 +48,14 @@ def _declare(L: C.CDLL) -> None:
         "v3o_partial_swiglu_int4": (None, [P, P, P, P, S, S]),
         "v3o_weighted_accumulate_f32": (None, [P, P, F, S]),
         "v3o_weighted_accumulate_f16": (None, [P, P, F, S]),
+        "v3o_fp4_e8m0_of_amax": (C.c_uint8, [F]),
+        "v3o_e2m1_rne": (C.c_uint8, [F]),
+        "v3o_exp_cw": (F, [F]),
+        "v3o_fp4_quantize_act": (None, [P, S, P, P]),
+        "v3o_nvfp4_matvec": (None, [P, P, P, P, S, S, P]),
+        "v3o_moe_experts_fused": (None, [P, P, P, P, P, S, S, S, S, P]),
+        "v3o_fp4_split_half": (None, [P, S]),
+        "v3o_fp4_to_tiled": (None, [P, P, S, S]),
         "v3o_router": (I, [P, P, I, S, S, S, I, F, I, P, P, P, P, I]),
         "v3o_quantize_int4": (None, [P, S, S, S, P]),
         "v3o_dequantize_int4": (None, [P, S, S, S, I, P]),
@@ -333,3 +341,72 @@ def moe_mxfp4_batched(x, hidden, inter, pages, ids, weights, nthreads=0) -> np.n
     lib().v3o_moe_mxfp4_batched(_p(x), tokens, hidden, inter, C.cast(arr, C.c_void_p),
                                 len(pages), _p(ids), _p(weights), top_k, _p(out), nthreads)
     return out
+
+
+# ---------------------------------------------------------------- NVFP4 fused MoE
+
+def fp4_e8m0_of_amax(amax: float) -> int:
+    return int(lib().v3o_fp4_e8m0_of_amax(float(amax)))
+
+
+def e2m1_rne(v: float) -> int:
+    return int(lib().v3o_e2m1_rne(float(v)))
+
+
+def exp_cw(x: float) -> float:
+    return float(lib().v3o_exp_cw(float(x)))
+
+
+def fp4_quantize_act(x) -> tuple:
+    """kernels.cu:3193 activation quantizer: (split-half codes, E8M0 scales)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    g = (x.size + 31) // 32
+    codes = np.zeros(g * 16, dtype=np.uint8)
+    sc = np.zeros(g, dtype=np.uint8)
+    lib().v3o_fp4_quantize_act(_p(x), x.size, _p(codes), _p(sc))
+    return codes, sc
+
+
+def nvfp4_matvec(act_codes, act_scales, data, scales, m, k) -> np.ndarray:
+    out = np.empty(m, dtype=np.float32)
+    a = np.ascontiguousarray(act_codes, dtype=np.uint8)
+    s = np.ascontiguousarray(act_scales, dtype=np.uint8)
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    w = np.ascontiguousarray(scales, dtype=np.uint16)
+    lib().v3o_nvfp4_matvec(_p(a), _p(s), _p(d), _p(w), m, k, _p(out))
+    return out
+
+
+def moe_experts_fused(act_codes, act_scales, experts, weights, k_in, m_mid, m_out, out):
+    """experts: per active expert ((up_data, up_scales), (gate_data, gate_scales),
+    (down_data, down_scales)); out (f32 [m_out]) accumulated in place."""
+    keep = []
+    dp = (C.c_void_p * (3 * len(experts)))()
+    sp = (C.c_void_p * (3 * len(experts)))()
+    for e, mats in enumerate(experts):
+        for s, (d, w) in enumerate(mats):
+            d = np.ascontiguousarray(d, dtype=np.uint8)
+            w = np.ascontiguousarray(w, dtype=np.uint16)
+            keep += [d, w]
+            dp[e * 3 + s] = d.ctypes.data
+            sp[e * 3 + s] = w.ctypes.data
+    wt = np.ascontiguousarray(weights, dtype=np.float32)
+    a = np.ascontiguousarray(act_codes, dtype=np.uint8)
+    sc = np.ascontiguousarray(act_scales, dtype=np.uint8)
+    assert out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
+    lib().v3o_moe_experts_fused(_p(a), _p(sc), dp, sp, _p(wt), len(experts), k_in, m_mid, m_out,
+                                _p(out))
+    return out
+
+
+def fp4_split_half(data) -> np.ndarray:
+    d = np.array(data, dtype=np.uint8, copy=True)
+    lib().v3o_fp4_split_half(_p(d), d.size)
+    return d
+
+
+def fp4_to_tiled(src, m, k) -> np.ndarray:
+    s = np.ascontiguousarray(src, dtype=np.uint8)
+    dst = np.zeros(m * k // 2, dtype=np.uint8)
+    lib().v3o_fp4_to_tiled(_p(s), _p(dst), m, k)
+    return dst

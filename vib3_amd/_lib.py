@@ -115,6 +115,13 @@ SIGNATURES = {
     "vib3_file_read_page": (I, [P, C.c_uint32, P, S, P]),
     "vib3_build_page_table": (I, [P, C.c_uint16, P, I, P, P, P, I, P, P]),
     "vib3_build_page_table_resolved": (I, [P, S, P, I, P, P, P, I, P, P, I, P]),
+    "vib3_launch_quantize_activation_fp4": (I, [P, P, P, I, P]),
+    "vib3_launch_quantize_activation_fp4_fast": (I, [P, P, P, I, P]),
+    "vib3_moe_prewarm_gpu_bufs": (I, [I, I]),
+    "vib3_launch_moe_experts_fused": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, P, P]),
+    "vib3_launch_moe_experts_fused_gpu": (I, [P, P, P, P, P, I, I, I, I, I, I, I, P, P]),
+    "vib3_launch_repack_weights_inplace": (I, [P, C.c_longlong, P]),
+    "vib3_launch_repack_row_to_tiled": (I, [P, P, I, I, P]),
     "vib3_hip_version": (C.c_char_p, []),
 }
 

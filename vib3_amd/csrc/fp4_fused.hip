@@ -1,0 +1,583 @@
+// fp4_fused.hip — the reference's sync-free fused MoE over NVFP4 pages (E2M1 weights with
+// per-32 block scales, FP4-quantized activations), rebuilt for gfx950:
+//   vib3_launch_quantize_activation_fp4[_fast]  (kernels.cu:3193-3266, :5252)
+//   vib3_launch_moe_experts_fused[_gpu]          (kernels.cu:5650, :5868; cuda_ffi.rs:809, :831)
+//   vib3_moe_prewarm_gpu_bufs                    (kernels.cu:6507; cuda_ffi.rs:1026)
+//   vib3_launch_repack_weights_inplace           (kernels.cu:4132-4183; cuda_ffi.rs:662)
+//   vib3_launch_repack_row_to_tiled              (kernels.cu:4185-4262; cuda_ffi.rs:718)
+//
+// Data formats (the contract of the reference's pages and activations):
+//   * split-half E2M1: per group of 32 values, 16 bytes; byte j holds value j in its low
+//     nibble and value j + 16 in its high nibble (kernels.cu:4125-4131);
+//   * tiled weight data: 16-row x 64-column tiles of 512 bytes, tile (rb, t) at
+//     (rb * K/64 + t) * 512, row r of the tile at + 32 r, its two groups at +0 / +16
+//     (kernels.cu:4185-4197);
+//   * weight scales after the data: [rows][K/32] 2-byte values read as E8M0 = (s >> 7) & 0xff,
+//     the exponent byte of a bf16 (kernels.cu:5404-5411); activation scales: E8M0 bytes;
+//   * E8M0 e is the power of two 2^(e - 127) (kernels.cu:2770-2777).
+//
+// Arithmetic: a group's dot product of 32 E2M1 x E2M1 products is an exact multiple of 1/4
+// (|.| <= 1152), so it is formed exactly in f32 with v_dot2_f32_f16 on decoded pairs, scaled by
+// the exact power of two 2^(ew + ea - 254) and accumulated in f64; the row sum is rounded to
+// f32 once. The result is therefore independent of the summation order (the reference sums
+// with MMA and K-parallel atomics, whose order varies run to run) and equals the oracle's
+// exactly. SwiGLU uses a Cody-Waite / Taylor exp of this file (the same operations as the
+// oracle, no contraction), so the FP4 intermediate is bit-identical to the oracle's too.
+#include <mutex>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace vib3 {
+namespace {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kFp4MaxActive = 8;  // MOE_MAX_EXPERTS (kernels.cu:5331)
+
+// ------------------------------------------------------------------------- scalar pieces
+
+// E8M0 exponent of a group's scale from its absolute maximum (kernels.cu:2759-2768):
+// round(log2(amax)) - 2 + 127 clamped to [0, 254], with round(log2) taken exactly as
+// floor(log2) + (mantissa > sqrt 2) (the float just below sqrt 2 has mantissa 0x3504f3).
+__device__ __forceinline__ uint32_t e8m0_of_amax(float amax) {
+  if (!(amax > 0.0f)) return 0;
+  const uint32_t b = __float_as_uint(amax);
+  const int E = (int)(b >> 23);
+  if (E == 0) return 0;  // subnormal: log2 < -126, below the clamp
+  const int n = E - 127 + ((b & 0x7fffff) > 0x3504f3 ? 1 : 0);
+  const int biased = n + 125;
+  return (uint32_t)(biased < 0 ? 0 : biased > 254 ? 254 : biased);
+}
+
+// Round-to-nearest-even onto the E2M1 grid {0, .5, 1, 1.5, 2, 3, 4, 6}, saturating at 6,
+// sign kept (cvt.rn.satfinite semantics of __nv_fp4x4_e2m1, used at kernels.cu:3227).
+__device__ __forceinline__ uint32_t e2m1_rne(float v) {
+  const uint32_t sign = (__float_as_uint(v) >> 31) << 3;
+  const float a = fabsf(v);
+  uint32_t c;
+  if (a <= 0.25f) c = 0;
+  else if (a < 0.75f) c = 1;
+  else if (a <= 1.25f) c = 2;
+  else if (a < 1.75f) c = 3;
+  else if (a <= 2.5f) c = 4;
+  else if (a < 3.5f) c = 5;
+  else if (a <= 5.0f) c = 6;
+  else c = 7;
+  return sign | c;
+}
+
+// 1 / 2^(e - 127), the exact reciprocal of an E8M0 scale (e = 0 reads as 0 there, whose
+// reciprocal is +inf, kernels.cu:2770-2777 with __frcp_rn).
+__device__ __forceinline__ float e8m0_inv(uint32_t e) {
+  return e == 0 ? __builtin_huge_valf() : __uint_as_float((254u - e) << 23);
+}
+
+// e^x by Cody-Waite reduction x = n ln2 + r (ln2 split in a 15-bit head and a tail, so n * head
+// is exact) and the degree-7 Taylor polynomial of e^r on |r| <= ln2 / 2 in Horner form, then
+// ldexp. Every operation is a single IEEE rounding (no contraction), so the oracle's C version
+// gives the same bits; within 2 ulp of the correctly rounded exp (tested against libm).
+__device__ __forceinline__ float exp_cw(float x) {
+#pragma clang fp contract(off)
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_huge_valf();
+  if (x < -103.97208404541015625f) return 0.0f;
+  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+  float r = x - n * 0.693145751953125f;
+  r = r - n * 1.428606765330187045e-06f;
+  float p = 1.0f / 5040.0f;
+  p = p * r + 1.0f / 720.0f;
+  p = p * r + 1.0f / 120.0f;
+  p = p * r + 1.0f / 24.0f;
+  p = p * r + 1.0f / 6.0f;
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  return __builtin_ldexpf(p, (int)n);
+}
+
+// h = (g * sigmoid(g)) * u, sigmoid(g) = 1 / (1 + e^-g), in the reference's order
+// (kernels.cu:5485-5487).
+__device__ __forceinline__ float swiglu_fp4(float g, float u) {
+#pragma clang fp contract(off)
+  const float sig = 1.0f / (1.0f + exp_cw(-g));
+  return (g * sig) * u;
+}
+
+// 2^(e) as a double for e in [-254, 254] (always a normal double: exact).
+__device__ __forceinline__ double pow2d(int e) {
+  return __longlong_as_double((long long)(e + 1023) << 52);
+}
+
+// Sixteen split-half bytes (one group) as sixteen f16 pairs (value j, value j + 16), exact.
+__device__ __forceinline__ void decode_group(const uint4 w, f16x2 (&o)[16]) {
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    o[4 * i + 0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 0);
+    o[4 * i + 1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 1);
+    o[4 * i + 2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 2);
+    o[4 * i + 3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 3);
+  }
+}
+
+// Exact group dot product of weight bytes `w` with a decoded activation group in LDS.
+__device__ __forceinline__ float group_dot(const uint4 w, const uint4* act) {
+  const uint4 a4[4] = {act[0], act[1], act[2], act[3]};
+  const uint32_t aw[16] = {a4[0].x, a4[0].y, a4[0].z, a4[0].w, a4[1].x, a4[1].y, a4[1].z, a4[1].w,
+                           a4[2].x, a4[2].y, a4[2].z, a4[2].w, a4[3].x, a4[3].y, a4[3].z, a4[3].w};
+  f16x2 wp[16];
+  decode_group(w, wp);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; j++)
+    s = __builtin_amdgcn_fdot2(wp[j], __builtin_bit_cast(f16x2, aw[j]), s, false);
+  return s;
+}
+
+// ------------------------------------------------------------------------- arguments
+
+struct Fp4Mat {
+  const uint8_t* data;     // tiled split-half codes
+  const uint16_t* scales;  // [rows][K/32]
+};
+
+struct Fp4Args {
+  const uint8_t* act;     // [K_in/2] split-half codes of the activation
+  const uint8_t* act_sc;  // [K_in/32] E8M0
+  // device-table form (moe_experts_fused_gpu): page = table[(layer * E + id) * 3 + seg]
+  const uint64_t* table;
+  const uint16_t* ids;
+  const float* wts_dev;
+  int layer, E;
+  // host-pointer form (moe_experts_fused): per slot up, gate, down
+  Fp4Mat mat[kFp4MaxActive][3];
+  float wts[kFp4MaxActive];
+  int n;                  // active experts
+  int K_in, M_mid, M_out;
+  uint8_t* mid;           // per slot: [M_mid/2] codes, then [M_mid/32] E8M0 (stride mid_stride)
+  size_t mid_stride;
+  float* out;             // [M_out] += sum_e w_e * down_e(h_e)
+};
+
+// Matrix `seg` of slot s, or {null, null} when the slot's id or page is not usable.
+__device__ __forceinline__ Fp4Mat slot_mat(const Fp4Args& a, int s, int seg, int rows, int K) {
+  if (!a.table) return a.mat[s][seg];
+  const int id = (int)a.ids[s];
+  if (id >= a.E) return Fp4Mat{nullptr, nullptr};
+  const uint64_t page = a.table[((size_t)a.layer * a.E + id) * 3 + seg];
+  if (!page) return Fp4Mat{nullptr, nullptr};
+  const uint8_t* p = (const uint8_t*)(uintptr_t)page;
+  return Fp4Mat{p, (const uint16_t*)(p + (size_t)(K / 2) * rows)};
+}
+
+// Decode `groups` split-half groups (codes + E8M0 bytes) into LDS pairs and exponents.
+__device__ __forceinline__ void stage_groups(const uint8_t* codes, const uint8_t* sc, int groups,
+                                             uint4* lds_pairs, int* lds_exp) {
+  for (int g = (int)threadIdx.x; g < groups; g += (int)blockDim.x) {
+    const uint4 w = *(const uint4*)(codes + (size_t)g * 16);
+    f16x2 p[16];
+    decode_group(w, p);
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      lds_pairs[(size_t)g * 4 + q] =
+          make_uint4(__builtin_bit_cast(uint32_t, p[4 * q]), __builtin_bit_cast(uint32_t, p[4 * q + 1]),
+                     __builtin_bit_cast(uint32_t, p[4 * q + 2]), __builtin_bit_cast(uint32_t, p[4 * q + 3]));
+    lds_exp[g] = (int)sc[g];
+  }
+}
+
+// Partial row sums of one 16-row block over tile pairs [p0, p1) of a tiled matrix: lane l owns
+// row l & 15 and, within each 1 KB pair of tiles, group (l >> 4) (bytes at (gg >> 1) * 512 +
+// row * 32 + (gg & 1) * 16: one load instruction reads the pair's whole kilobyte). Returns the
+// lane's f64 partial; the four lanes of a row are summed by the caller.
+__device__ __forceinline__ double block_rows(const Fp4Mat m, int rb, int nkt, int G, int p0,
+                                             int p1, const uint4* act_pairs, const int* act_exp) {
+  const int lane = lane_id();
+  const int row = lane & 15, gg = lane >> 4;
+  const uint8_t* base = m.data + ((size_t)rb * nkt) * 512 + (gg >> 1) * 512 + row * 32 + (gg & 1) * 16;
+  const uint16_t* srow = m.scales + (size_t)(rb * 16 + row) * G;
+  double acc = 0.0;
+  // two pairs in flight: pair p + 1 loads while pair p is reduced
+  uint4 w0 = make_uint4(0, 0, 0, 0);
+  uint16_t s0 = 0;
+  if (p0 < p1) {
+    w0 = ld_stream(base + (size_t)p0 * 1024);
+    s0 = ld_u16(srow + 4 * p0 + gg);
+  }
+  for (int p = p0; p < p1; p++) {
+    uint4 w1 = w0;
+    uint16_t s1 = s0;
+    if (p + 1 < p1) {
+      w1 = ld_stream(base + (size_t)(p + 1) * 1024);
+      s1 = ld_u16(srow + 4 * (p + 1) + gg);
+    }
+    const int g = 4 * p + gg;
+    const float sdot = group_dot(w0, act_pairs + (size_t)g * 4);
+    acc = fma((double)sdot, pow2d((int)((s0 >> 7) & 0xff) + act_exp[g] - 254), acc);
+    w0 = w1;
+    s0 = s1;
+  }
+  return acc;
+}
+
+__device__ __forceinline__ double shfl_xor_d(double v, int m) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __shfl_xor((int)(uint32_t)b, m), hi = __shfl_xor((int)(uint32_t)(b >> 32), m);
+  return __longlong_as_double(((long long)hi << 32) | (uint32_t)lo);
+}
+
+// ------------------------------------------------------------------------- kernels
+
+// Activation quantizer (kernels.cu:3193-3240): per group of 32, E8M0 from the absolute maximum,
+// values times 1/scale rounded to E2M1, packed split-half. One thread per group.
+__global__ void k_fp4_quant_act(const float* x, uint8_t* codes, uint8_t* scales, int K) {
+  const int g = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (g * 32 >= K) return;
+  float v[32];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    v[i] = g * 32 + i < K ? x[g * 32 + i] : 0.0f;
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  const uint32_t e = e8m0_of_amax(amax);
+  const float inv = amax == 0.0f ? 0.0f : e8m0_inv(e);
+  uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    const uint32_t byte = e2m1_rne(v[j] * inv) | (e2m1_rne(v[j + 16] * inv) << 4);
+    w[j >> 2] |= byte << (8 * (j & 3));
+  }
+  if ((K & 31) == 0 || g * 32 + 32 <= K) {
+    *(uint4*)(codes + (size_t)g * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {  // a ragged last group: only its bytes
+    for (int j = 0; j < 16 && g * 32 + j < K; j++) codes[(size_t)g * 16 + j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+  }
+  scales[g] = (uint8_t)e;
+}
+
+// Gate/up of every active expert + SwiGLU + FP4 quantization of h (kernels.cu:5357-5517 fused):
+// workgroup (q, s) = 32 rows [32q, 32q + 32) of slot s; wave w takes row block 2q + (w >> 2)
+// and k quarter w & 3 of both matrices; the quarters meet in LDS, and the 32 rows, one E8M0
+// group of h, are quantized and written split-half.
+__global__ __launch_bounds__(512) void k_fp4_gateup(Fp4Args a) {
+  extern __shared__ uint4 lds[];
+  const int Gin = a.K_in / 32, nkt = a.K_in / 64, P = nkt / 2;
+  uint4* act_pairs = lds;                               // [Gin][4]
+  int* act_exp = (int*)(lds + (size_t)Gin * 4);         // [Gin]
+  __shared__ double part[8][16][2];
+  __shared__ float hrow[32];
+  const int s = (int)blockIdx.y, q = (int)blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = lane_id();
+  const Fp4Mat up = slot_mat(a, s, 0, a.M_mid, a.K_in);
+  const Fp4Mat gate = slot_mat(a, s, 1, a.M_mid, a.K_in);
+  uint8_t* hcodes = a.mid + (size_t)s * a.mid_stride;
+  uint8_t* hsc = hcodes + a.M_mid / 2;
+  if (!up.data || !gate.data || !up.scales || !gate.scales) {  // unusable slot: h = 0
+    if (threadIdx.x < 16) hcodes[(size_t)q * 16 + threadIdx.x] = 0;
+    if (threadIdx.x == 0) hsc[q] = 0;
+    return;
+  }
+  stage_groups(a.act, a.act_sc, Gin, act_pairs, act_exp);
+  __syncthreads();
+  const int rb = 2 * q + (wave >> 2), kq = wave & 3;
+  const int p0 = kq * P / 4, p1 = (kq + 1) * P / 4;
+  double u = block_rows(up, rb, nkt, Gin, p0, p1, act_pairs, act_exp);
+  double g = block_rows(gate, rb, nkt, Gin, p0, p1, act_pairs, act_exp);
+  u += shfl_xor_d(u, 16);
+  g += shfl_xor_d(g, 16);
+  u += shfl_xor_d(u, 32);
+  g += shfl_xor_d(g, 32);
+  if (lane < 16) {
+    part[wave][lane][0] = u;
+    part[wave][lane][1] = g;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // lane t < 32: row 32q + t = row block 2q + (t >> 4), row t & 15; quarters in order
+    const int t = lane & 31, w0 = (t >> 4) * 4;
+    double su = 0.0, sg = 0.0;
+    for (int k = 0; k < 4; k++) {
+      su += part[w0 + k][t & 15][0];
+      sg += part[w0 + k][t & 15][1];
+    }
+    const float h = swiglu_fp4((float)sg, (float)su);
+    // E8M0 of the 32 rows (lanes 0..31 and their copies 32..63 give the same maximum)
+    float amax = fabsf(h);
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+    const uint32_t e = e8m0_of_amax(amax);
+    const float inv = amax == 0.0f ? 0.0f : e8m0_inv(e);
+    const uint32_t code = e2m1_rne(h * inv);
+    const uint32_t hi = (uint32_t)__shfl(code, (lane & 15) + 16);
+    if (lane < 16) hcodes[(size_t)q * 16 + lane] = (uint8_t)(code | (hi << 4));
+    if (lane == 0) hsc[q] = (uint8_t)e;
+    (void)hrow;
+  }
+}
+
+// Down of every active expert + weighted accumulate (kernels.cu:5519-5591): workgroup rb =
+// output rows [16 rb, 16 rb + 16); wave s = slot s over the whole K_mid; the slots' results
+// meet in LDS and out[r] += w_s * d_s[r] in slot order.
+__global__ __launch_bounds__(512) void k_fp4_down(Fp4Args a) {
+  extern __shared__ uint4 lds[];
+  const int Gm = a.M_mid / 32, nkt = a.M_mid / 64, P = nkt / 2;
+  uint4* hp = lds;                                        // [n][Gm][4]
+  int* he = (int*)(lds + (size_t)a.n * Gm * 4);           // [n][Gm]
+  __shared__ float d[kFp4MaxActive][16];
+  const int rb = (int)blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = lane_id();
+  for (int s = 0; s < a.n; s++) {
+    const uint8_t* hc = a.mid + (size_t)s * a.mid_stride;
+    stage_groups(hc, hc + a.M_mid / 2, Gm, hp + (size_t)s * Gm * 4, he + (size_t)s * Gm);
+  }
+  __syncthreads();
+  const int s = wave;
+  float ds = 0.0f;
+  bool use = false;
+  if (s < a.n) {
+    const Fp4Mat dn = slot_mat(a, s, 2, a.M_out, a.M_mid);
+    use = dn.data && dn.scales;
+    if (use) {
+      double acc = block_rows(dn, rb, nkt, Gm, 0, P, hp + (size_t)s * Gm * 4, he + (size_t)s * Gm);
+      acc += shfl_xor_d(acc, 16);
+      acc += shfl_xor_d(acc, 32);
+      ds = (float)acc;
+    }
+    if (lane < 16) d[s][lane] = use ? ds : 0.0f;
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int r = rb * 16 + (int)threadIdx.x;
+    float o = a.out[r];
+    for (int t = 0; t < a.n; t++) {
+      float w;
+      if (a.table) {
+        const int id = (int)a.ids[t];
+        if (id >= a.E || !a.table[((size_t)a.layer * a.E + id) * 3 + 2]) continue;
+        w = a.wts_dev[t];
+      } else {
+        if (!a.mat[t][2].data || !a.mat[t][2].scales) continue;
+        w = a.wts[t];
+      }
+      o = add_mul_rn(o, w, d[t][threadIdx.x]);
+    }
+    a.out[r] = o;
+  }
+}
+
+// Sequential -> split-half within every 16-byte block (kernels.cu:4125-4160).
+__global__ void k_fp4_split_half(uint8_t* data, long long nblocks) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nblocks) return;
+  uint4* p = (uint4*)(data + i * 16);
+  const uint4 v = *p;
+  const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+  uint32_t out[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint32_t s0 = (in[j >> 2] >> (8 * (j & 3))) & 0xff;
+    const uint32_t s1 = (in[(j + 8) >> 2] >> (8 * ((j + 8) & 3))) & 0xff;
+    const uint32_t b0 = (s0 & 0x0f) | ((s1 & 0x0f) << 4);
+    const uint32_t b1 = (s0 >> 4) | (s1 & 0xf0);
+    out[(2 * j) >> 2] |= b0 << (8 * ((2 * j) & 3));
+    out[(2 * j + 1) >> 2] |= b1 << (8 * ((2 * j + 1) & 3));
+  }
+  *p = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+// Row-major split-half [M][K/2] -> tiled (kernels.cu:4190-4225): one 32-byte row piece per thread.
+__global__ void k_fp4_to_tiled(const uint8_t* src, uint8_t* dst, int M, int pk) {
+  const int nkt = pk / 32;
+  const long long total = (long long)(M / 16) * nkt * 16;
+  const long long c = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= total) return;
+  const int r_in = (int)(c % 16);
+  const long long tile = c / 16;
+  const int t = (int)(tile % nkt);
+  const long long rb = tile / nkt;
+  const long long row = rb * 16 + r_in;
+  const uint4* s = (const uint4*)(src + row * pk + (long long)t * 32);
+  uint4* o = (uint4*)(dst + (rb * nkt + t) * 512 + (long long)r_in * 32);
+  o[0] = s[0];
+  o[1] = s[1];
+}
+
+// ------------------------------------------------------------------------- host side
+
+// Per-device intermediate buffer of the fused layer (h of every slot, FP4 + E8M0), allocated by
+// vib3_moe_prewarm_gpu_bufs only: the launches never allocate.
+struct MidBuf {
+  uint8_t* ptr = nullptr;
+  size_t stride = 0;  // bytes per slot
+  int max_mid = 0;
+};
+MidBuf g_mid[64];
+std::mutex g_mid_lock;
+
+size_t mid_stride(int m_mid) { return ((size_t)m_mid / 2 + (size_t)m_mid / 32 + 255) / 256 * 256; }
+
+int current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -1;
+  return dev;
+}
+
+// Shape limits of the fused kernels: tiles of 16 rows x 64 columns taken in 128-column pairs,
+// 32-row E8M0 groups of h, decoded activations / intermediates within 64 KB of LDS.
+int check_shape(int n, int K_in, int M_mid, int K_mid, int M_out) {
+  if (n <= 0 || n > kFp4MaxActive) return VIB3_ERR_BAD_COUNT;  // kernels.cu:5672
+  if (K_in <= 0 || M_mid <= 0 || M_out <= 0 || K_mid != M_mid) return VIB3_ERR_BAD_COUNT;
+  if (K_in % 128 || M_mid % 128 || M_out % 16) return VIB3_ERR_UNSUPPORTED;
+  if ((size_t)K_in * 2 + K_in / 8 > 65536) return VIB3_ERR_UNSUPPORTED;
+  if ((size_t)n * M_mid * 2 + (size_t)n * M_mid / 8 > 65536) return VIB3_ERR_UNSUPPORTED;
+  return 0;
+}
+
+int launch_fused(Fp4Args& a, hipStream_t st) {
+  const int dev = current_device();
+  if (dev < 0) return VIB3_ERR_BAD_POINTER;
+  const MidBuf mb = g_mid[dev];
+  if (!mb.ptr || mb.max_mid < a.M_mid) return VIB3_ERR_WORKSPACE;  // not prewarmed
+  a.mid = mb.ptr;
+  a.mid_stride = mb.stride;
+  const int Gin = a.K_in / 32, Gm = a.M_mid / 32;
+  hipLaunchKernelGGL(k_fp4_gateup, dim3((unsigned)(a.M_mid / 32), (unsigned)a.n), dim3(512),
+                     (unsigned)((size_t)Gin * 64 + (size_t)Gin * 4), st, a);
+  hipLaunchKernelGGL(k_fp4_down, dim3((unsigned)(a.M_out / 16)), dim3(64 * a.n),
+                     (unsigned)((size_t)a.n * Gm * 64 + (size_t)a.n * Gm * 4), st, a);
+  VIB3_RETURN_LAUNCH();
+}
+
+}  // namespace
+}  // namespace vib3
+
+using namespace vib3;
+
+extern "C" {
+
+int vib3_launch_quantize_activation_fp4(const void* input, void* act_fp4, void* act_scales,
+                                        int K, void* stream) {
+  if (K <= 0) return VIB3_ERR_BAD_COUNT;
+  if (!input || !act_fp4 || !act_scales) return VIB3_ERR_BAD_POINTER;
+  if (((uintptr_t)act_fp4 & 15)) return VIB3_ERR_BAD_POINTER;
+  const int groups = (K + 31) / 32;
+  hipLaunchKernelGGL(k_fp4_quant_act, dim3((unsigned)((groups + 63) / 64)), dim3(64), 0,
+                     (hipStream_t)stream, (const float*)input, (uint8_t*)act_fp4,
+                     (uint8_t*)act_scales, K);
+  VIB3_RETURN_LAUNCH();
+}
+
+int vib3_launch_quantize_activation_fp4_fast(const void* input, void* act_fp4, void* act_scales,
+                                             int K, void* stream) {
+  return vib3_launch_quantize_activation_fp4(input, act_fp4, act_scales, K, stream);
+}
+
+int vib3_moe_prewarm_gpu_bufs(int m_mid, int k_mid) {
+  if (m_mid <= 0 || k_mid <= 0) return VIB3_ERR_BAD_COUNT;
+  const int mid = m_mid > k_mid ? m_mid : k_mid;
+  const int dev = current_device();
+  if (dev < 0) return VIB3_ERR_BAD_POINTER;
+  std::lock_guard<std::mutex> lock(g_mid_lock);
+  MidBuf& mb = g_mid[dev];
+  if (mb.ptr && mb.max_mid >= mid) return 0;
+  const size_t stride = mid_stride(mid);
+  void* p = nullptr;
+  const hipError_t e = hipMalloc(&p, stride * kFp4MaxActive);
+  if (e != hipSuccess) return (int)e;
+  // the previous buffer stays allocated: a launch already queued may still read it
+  mb.ptr = (uint8_t*)p;
+  mb.stride = stride;
+  mb.max_mid = mid;
+  return 0;
+}
+
+int vib3_launch_moe_experts_fused(const void* act_fp4, const void* act_scales,
+                                  const void* const* up_weight_ptrs,
+                                  const void* const* up_scale_ptrs,
+                                  const void* const* gate_weight_ptrs,
+                                  const void* const* gate_scale_ptrs,
+                                  const void* const* down_weight_ptrs,
+                                  const void* const* down_scale_ptrs,
+                                  const float* expert_weights_host, int num_experts, int K_in,
+                                  int M_mid, int K_mid, int M_out, float* layer_output,
+                                  void* stream) {
+  const int rc = check_shape(num_experts, K_in, M_mid, K_mid, M_out);
+  if (rc) return rc;
+  if (!act_fp4 || !act_scales || !up_weight_ptrs || !up_scale_ptrs || !gate_weight_ptrs ||
+      !gate_scale_ptrs || !down_weight_ptrs || !down_scale_ptrs || !expert_weights_host ||
+      !layer_output)
+    return VIB3_ERR_BAD_POINTER;
+  Fp4Args a{};
+  a.act = (const uint8_t*)act_fp4;
+  a.act_sc = (const uint8_t*)act_scales;
+  a.n = num_experts;
+  a.K_in = K_in; a.M_mid = M_mid; a.M_out = M_out;
+  a.out = layer_output;
+  for (int s = 0; s < num_experts; s++) {
+    a.mat[s][0] = Fp4Mat{(const uint8_t*)up_weight_ptrs[s], (const uint16_t*)up_scale_ptrs[s]};
+    a.mat[s][1] = Fp4Mat{(const uint8_t*)gate_weight_ptrs[s], (const uint16_t*)gate_scale_ptrs[s]};
+    a.mat[s][2] = Fp4Mat{(const uint8_t*)down_weight_ptrs[s], (const uint16_t*)down_scale_ptrs[s]};
+    a.wts[s] = expert_weights_host[s];
+  }
+  return launch_fused(a, (hipStream_t)stream);
+}
+
+int vib3_launch_moe_experts_fused_gpu(const void* act_fp4, const void* act_scales,
+                                      const uint64_t* page_table, const uint16_t* expert_ids,
+                                      const float* expert_weights, int layer,
+                                      int num_experts_total, int num_active, int K_in, int M_mid,
+                                      int K_mid, int M_out, float* layer_output, void* stream) {
+  const int rc = check_shape(num_active, K_in, M_mid, K_mid, M_out);
+  if (rc) return rc;
+  if (layer < 0 || num_experts_total <= 0) return VIB3_ERR_BAD_COUNT;
+  if (!act_fp4 || !act_scales || !page_table || !expert_ids || !expert_weights || !layer_output)
+    return VIB3_ERR_BAD_POINTER;
+  Fp4Args a{};
+  a.act = (const uint8_t*)act_fp4;
+  a.act_sc = (const uint8_t*)act_scales;
+  a.table = page_table;
+  a.ids = expert_ids;
+  a.wts_dev = expert_weights;
+  a.layer = layer;
+  a.E = num_experts_total;
+  a.n = num_active;
+  a.K_in = K_in; a.M_mid = M_mid; a.M_out = M_out;
+  a.out = layer_output;
+  return launch_fused(a, (hipStream_t)stream);
+}
+
+int vib3_launch_repack_weights_inplace(void* weight_data_ptr, long long weight_data_bytes,
+                                       void* stream) {
+  if (weight_data_bytes < 0) return VIB3_ERR_BAD_COUNT;
+  if (!weight_data_ptr || ((uintptr_t)weight_data_ptr & 15)) return VIB3_ERR_BAD_POINTER;
+  const long long nblocks = weight_data_bytes / 16;  // a partial last block is left as it is
+  if (nblocks == 0) return 0;
+  hipLaunchKernelGGL(k_fp4_split_half, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (uint8_t*)weight_data_ptr, nblocks);
+  VIB3_RETURN_LAUNCH();
+}
+
+int vib3_launch_repack_row_to_tiled(void* weight_data_ptr, void* temp_buf, int M, int K,
+                                    void* stream) {
+  if (M < 0 || K < 0) return VIB3_ERR_BAD_COUNT;
+  if (M % 16 || K % 64) return VIB3_ERR_UNSUPPORTED;  // kernels.cu:4198
+  if (!weight_data_ptr || !temp_buf || ((uintptr_t)weight_data_ptr & 15) ||
+      ((uintptr_t)temp_buf & 15))
+    return VIB3_ERR_BAD_POINTER;
+  const int pk = K / 2;
+  const long long chunks = (long long)(M / 16) * (pk / 32) * 16;
+  if (chunks == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_fp4_to_tiled, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st,
+                     (const uint8_t*)weight_data_ptr, (uint8_t*)temp_buf, M, pk);
+  const hipError_t e = hipMemcpyAsync(weight_data_ptr, temp_buf, (size_t)M * pk,
+                                      hipMemcpyDeviceToDevice, st);
+  if (e != hipSuccess) return (int)e;
+  VIB3_RETURN_LAUNCH();
+}
+
+}  // extern "C"

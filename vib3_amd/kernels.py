@@ -12,8 +12,9 @@ the reference GPU behaviour is ``scale_dtype=DT_F16``.
 """
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass
-from typing import List, Optional, Tuple
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 
@@ -234,3 +235,78 @@ def run_router_gpu_topk(hidden_state, router_weights, num_experts, hidden_dim, t
     """kernels.rs:1811 run_router_gpu_topk (bias always NULL there)."""
     return run_router_with_scoring_and_bias(hidden_state, router_weights, num_experts, hidden_dim,
                                             top_k, scoring_func, scores_dev)
+
+
+# ---------------------------------------------------------------- NVFP4 fused MoE
+
+def quantize_activation_fp4(input: torch.Tensor, act_fp4: torch.Tensor, act_scales: torch.Tensor,
+                            k: int) -> None:
+    """kernels.rs:785 quantize_activation_fp4 (and :1486 _fast): f32 [k] -> split-half E2M1
+    codes [k/2] (16-byte aligned) + E8M0 scales [k/32]."""
+    if input.dtype != torch.float32:
+        raise TypeError("quantize_activation_fp4 takes an f32 input")
+    _lib.call("vib3_launch_quantize_activation_fp4", _dev(input, "input"),
+              _dev(act_fp4, "act_fp4"), _dev(act_scales, "act_scales"), k, _stream(input))
+
+
+quantize_activation_fp4_fast = quantize_activation_fp4
+
+
+def moe_prewarm_gpu_bufs(m_mid: int, k_mid: int) -> None:
+    """cuda_ffi.rs:1026 vib3_moe_prewarm_gpu_bufs: the fused MoE's intermediate buffer on the
+    current device (the one allocation of this path; call before graph capture)."""
+    _lib.call("vib3_moe_prewarm_gpu_bufs", m_mid, k_mid)
+
+
+def _nvfp4_data_bytes(k: int, m: int) -> int:
+    return ((k + 1) // 2) * m
+
+
+def moe_experts_fused(act_fp4: torch.Tensor, act_scales: torch.Tensor,
+                      expert_pages: Sequence[Tuple[int, int, int, float]], k_in: int, m_mid: int,
+                      m_out: int, layer_output: torch.Tensor) -> None:
+    """kernels.rs:1010 moe_experts_fused: expert_pages = (up_page, gate_page, down_page, weight)
+    with device addresses of tiled split-half NVFP4 pages (scales after the data); at most 8
+    are used; layer_output (f32 [m_out]) is accumulated."""
+    n = min(len(expert_pages), 8)
+    if n == 0:
+        raise ValueError("moe_experts_fused needs at least one expert")
+    arr = lambda: (C.c_void_p * 8)()
+    uw, us, gw, gs, dw, ds = arr(), arr(), arr(), arr(), arr(), arr()
+    w = (C.c_float * 8)()
+    up_sz, down_sz = _nvfp4_data_bytes(k_in, m_mid), _nvfp4_data_bytes(m_mid, m_out)
+    for i, (up, gate, down, wt) in enumerate(expert_pages[:n]):
+        uw[i], us[i] = up, up + up_sz
+        gw[i], gs[i] = gate, gate + up_sz
+        dw[i], ds[i] = down, down + down_sz
+        w[i] = wt
+    _lib.call("vib3_launch_moe_experts_fused", _dev(act_fp4, "act_fp4"),
+              _dev(act_scales, "act_scales"), uw, us, gw, gs, dw, ds, w, n, k_in, m_mid, m_mid,
+              m_out, _dev(layer_output, "layer_output"), _stream(layer_output))
+
+
+def moe_experts_fused_gpu(act_fp4: torch.Tensor, act_scales: torch.Tensor,
+                          page_table: torch.Tensor, expert_ids: torch.Tensor,
+                          expert_weights: torch.Tensor, moe_layer: int, num_experts_total: int,
+                          num_active: int, k_in: int, m_mid: int, m_out: int,
+                          layer_output: torch.Tensor) -> None:
+    """kernels.rs:1091 moe_experts_fused_gpu: ids / weights and the page table
+    u64[layers][experts][3] stay on the device (no host sync)."""
+    _lib.call("vib3_launch_moe_experts_fused_gpu", _dev(act_fp4, "act_fp4"),
+              _dev(act_scales, "act_scales"), _dev(page_table, "page_table"),
+              _dev(expert_ids, "expert_ids"), _dev(expert_weights, "expert_weights"), moe_layer,
+              num_experts_total, num_active, k_in, m_mid, m_mid, m_out,
+              _dev(layer_output, "layer_output"), _stream(layer_output))
+
+
+def repack_weights_inplace(weight_data: torch.Tensor, weight_data_bytes: int) -> None:
+    """kernels.rs:915: sequential -> split-half nibble order, in place."""
+    _lib.call("vib3_launch_repack_weights_inplace", _dev(weight_data, "weight_data"),
+              weight_data_bytes, _stream(weight_data))
+
+
+def repack_row_to_tiled(weight_data: torch.Tensor, temp_buf: torch.Tensor, m_slice: int,
+                        k: int) -> None:
+    """kernels.rs:1289: row-major split-half [m][k/2] -> 16x64 tiles, through temp_buf."""
+    _lib.call("vib3_launch_repack_row_to_tiled", _dev(weight_data, "weight_data"),
+              _dev(temp_buf, "temp_buf"), m_slice, k, _stream(weight_data))
