@@ -43,6 +43,11 @@ CONFIGS = {
                         "grouped per expert as a grouped GEMM on MFMA with fused SwiGLU, bf16 out",
                hidden=7168, inter=2048, E=384, k=8, tokens=64, zipf=1.1, seed=0x5EED0004,
                layers=2, batches=8),
+    "fp4": dict(workload="reference fused NVFP4 MoE (vib3_launch_moe_experts_fused_gpu, "
+                         "kernels.cu:5868) at Kimi-K2.5 shape: FP4 activation quantize + 8 of "
+                         "384 experts (tiled split-half E2M1, bf16-exponent scales per 32), "
+                         "hidden 7168, inter 2048, device page table u64[L][E][3]",
+                hidden=7168, inter=2048, E=384, k=8, seed=0x5EED0005, layers=4),
     "c1": dict(workload="c1: Mixtral-8x7B MoE layer decode, batch 1 (router fp32 [8,4096] softmax "
                         "top-2; 8 INT4 experts 14336x4096, g128 fp16 scales; x fp16)",
                hidden=4096, inter=14336, g=128, sdt="f16", sigma=0.02, E=8, shared=0, k=2,
@@ -219,6 +224,95 @@ def bench_c4(args, cfg) -> int:
     return 0
 
 
+def bench_fp4(args, cfg) -> int:
+    """The reference's sync-free fused NVFP4 path: a step = quantize the f32 activation to FP4
+    + vib3_launch_moe_experts_fused_gpu over 8 experts of a 384-expert layer (the launches the
+    engine issues per MoE layer, engine.rs:5143-5179)."""
+    import numpy as np
+    import torch
+
+    from vib3_amd import _hip, _lib
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream(dev).cuda_stream
+    H, I, E, K = cfg["hidden"], cfg["inter"], cfg["E"], cfg["k"]
+    L = args.layers or cfg["layers"]
+    g = torch.Generator(device=dev).manual_seed(cfg["seed"])
+    data_gu, data_dn = H // 2 * I, I // 2 * H
+    sc_gu, sc_dn = I * (H // 32) * 2, H * (I // 32) * 2
+    page = [data_gu + sc_gu, data_gu + sc_gu, data_dn + sc_dn]
+    ebytes = sum(page)
+    t0 = time.perf_counter()
+    pools, table = [], np.zeros((L, E, 3), dtype=np.uint64)
+    for l in range(L):
+        pool = torch.randint(0, 256, (E * ebytes,), dtype=torch.uint8, device=dev, generator=g)
+        base = pool.data_ptr()
+        per_e = pool.view(E, ebytes)
+        off = 0
+        for s in range(3):  # bf16 scales: exponent 119..123 (2^-8..2^-4), random mantissa
+            rows, k = (I, H) if s < 2 else (H, I)
+            table[l, :, s] = base + np.arange(E, dtype=np.uint64) * ebytes + off
+            sc = per_e[:, off + rows * k // 2: off + page[s]].view(torch.int16)
+            ex = torch.randint(119, 124, sc.shape, dtype=torch.int16, device=dev, generator=g)
+            sc.copy_((ex << 7) | (sc & 0x7F))
+            off += page[s]
+        pools.append(pool)
+        torch.cuda.synchronize()
+        log(f"[bench] fp4 layer {l} ready ({pool.numel() / 1e9:.2f} GB, {time.perf_counter() - t0:.1f}s)")
+    tab = torch.from_numpy(table.view(np.int64)).to(dev)
+    rng = np.random.default_rng(cfg["seed"])
+    T = args.tokens
+    xs = [torch.randn(H, dtype=torch.float32, device=dev, generator=g) for _ in range(T)]
+    ids = [torch.from_numpy(rng.choice(E, K, replace=False).astype(np.int16)).to(dev)
+           for _ in range(T)]
+    wts = torch.full((K,), 1.0 / K, dtype=torch.float32, device=dev)
+    codes = torch.zeros(H // 2, dtype=torch.uint8, device=dev)
+    scs = torch.zeros(H // 32, dtype=torch.uint8, device=dev)
+    out = torch.zeros(H, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    _lib.call("vib3_moe_prewarm_gpu_bufs", I, I)
+
+    def step(i):
+        rc = lib.vib3_launch_quantize_activation_fp4(xs[i % T].data_ptr(), codes.data_ptr(),
+                                                     scs.data_ptr(), H, st)
+        rc = rc or lib.vib3_launch_moe_experts_fused_gpu(
+            codes.data_ptr(), scs.data_ptr(), tab.data_ptr(), ids[i % T].data_ptr(),
+            wts.data_ptr(), i % L, E, K, H, I, I, H, out.data_ptr(), st)
+        if rc:
+            raise _lib.Vib3Error("fp4 fused step", rc)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = _hip.Event(), _hip.Event()
+    e0.record(st)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    e1.record(st)
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) * 1e3 / args.steps
+    nbytes = K * ebytes + H * 4 + H // 2 + H // 32 + 2 * H * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"[bench] fp4 fused: {us:.2f} us/layer, {gbs:.0f} GB/s")
+    out_line = {
+        "metric": "fused NVFP4 MoE layer decode us (batch 1, Kimi-K2.5 shape)",
+        "value": round(us, 3), "unit": "us/layer", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us / 1e3, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "e2m1 weights x e2m1 activations, exact group sums, f64/f32 accumulate",
+        "data": "synthetic (random codes, bf16 scales of exponent 2^-8..2^-4)",
+        "config": {"workload": cfg["workload"], "layers_rotated": L, "tokens": T,
+                   "algorithmic_bytes_per_layer": nbytes},
+        "roofline": {"bound": "hbm", "kernel": "k_fp4_quant_act + k_fp4_gateup + k_fp4_down (whole step)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out_line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -251,6 +345,8 @@ def main() -> int:
     cfg = dict(CONFIGS[args.config])
     if args.config == "c4":
         return bench_c4(args, cfg)
+    if args.config == "fp4":
+        return bench_fp4(args, cfg)
     if args.layers:
         cfg["layers"] = args.layers
     torch.cuda.set_device(0)

@@ -266,8 +266,8 @@ int vib3_launch_moe_int4_layer_stage(const vib3_moe_int4_layer *layer, int stage
  * vib3_launch_repack_row_to_tiled) followed by [rows][k/32] 2-byte scales whose exponent byte
  * (s >> 7 & 0xff, a bf16's) is the E8M0 block scale (kernels.cu:5404-5411). Sums are exact
  * (f64) and rounded once to f32, so results do not depend on launch order. Shapes: k_in and
- * m_mid multiples of 128, m_out of 16, k_mid == m_mid, k_in <= 32768 and
- * num_experts * m_mid <= 32768 (VIB3_ERR_UNSUPPORTED otherwise). A slot whose id is
+ * m_mid multiples of 128, m_out of 16, k_mid == m_mid, and each kernel's LDS within 64 KB:
+ * about k_in <= 15360 and num_experts * m_mid <= 24576 (VIB3_ERR_UNSUPPORTED otherwise). A slot whose id is
  * >= num_experts_total or whose table entry is 0 contributes nothing.
  * ---------------------------------------------------------------------------------------- */
 

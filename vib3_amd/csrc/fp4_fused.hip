@@ -34,6 +34,10 @@ namespace {
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kFp4MaxActive = 8;  // MOE_MAX_EXPERTS (kernels.cu:5331)
+#ifndef VIB3_FP4_DEPTH
+#define VIB3_FP4_DEPTH 2  // 1 KB tile pairs in flight per matrix stream (build-time knob)
+#endif
+constexpr int kFp4Depth = VIB3_FP4_DEPTH;
 
 // ------------------------------------------------------------------------- scalar pieces
 
@@ -171,11 +175,32 @@ __device__ __forceinline__ Fp4Mat slot_mat(const Fp4Args& a, int s, int seg, int
   return Fp4Mat{p, (const uint16_t*)(p + (size_t)(K / 2) * rows)};
 }
 
-// Decode `groups` split-half groups (codes + E8M0 bytes) into LDS pairs and exponents.
-__device__ __forceinline__ void stage_groups(const uint8_t* codes, const uint8_t* sc, int groups,
-                                             uint4* lds_pairs, int* lds_exp) {
-  for (int g = (int)threadIdx.x; g < groups; g += (int)blockDim.x) {
-    const uint4 w = *(const uint4*)(codes + (size_t)g * 16);
+// Decode split-half groups (codes + E8M0 bytes) into LDS pairs and exponents: group g of
+// `groups` goes to lds_pairs[g * 4 .. g * 4 + 3] / lds_exp[g]. Staging is split so the caller can
+// issue its first weight loads between the loads of the first R groups per thread (issue) and
+// their conversion (finish); finish() then stages any remaining groups directly.
+template <int R>
+struct Stage {
+  uint4 w[R];
+  uint8_t e[R];
+  const uint8_t* codes;
+  const uint8_t* sc;
+  int groups;
+
+  __device__ __forceinline__ void issue(const uint8_t* c, const uint8_t* s_, int n) {
+    codes = c;
+    sc = s_;
+    groups = n;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int g = min((int)threadIdx.x + r * (int)blockDim.x, n - 1);
+      w[r] = *(const uint4*)(codes + (size_t)g * 16);
+      e[r] = sc[g];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // these loads go out before anything issued later
+  }
+  __device__ __forceinline__ static void put(uint4* lds_pairs, int* lds_exp, int g, uint4 w,
+                                             uint8_t e) {
     f16x2 p[16];
     decode_group(w, p);
 #pragma unroll
@@ -183,42 +208,124 @@ __device__ __forceinline__ void stage_groups(const uint8_t* codes, const uint8_t
       lds_pairs[(size_t)g * 4 + q] =
           make_uint4(__builtin_bit_cast(uint32_t, p[4 * q]), __builtin_bit_cast(uint32_t, p[4 * q + 1]),
                      __builtin_bit_cast(uint32_t, p[4 * q + 2]), __builtin_bit_cast(uint32_t, p[4 * q + 3]));
-    lds_exp[g] = (int)sc[g];
+    lds_exp[g] = (int)e;
   }
-}
-
-// Partial row sums of one 16-row block over tile pairs [p0, p1) of a tiled matrix: lane l owns
-// row l & 15 and, within each 1 KB pair of tiles, group (l >> 4) (bytes at (gg >> 1) * 512 +
-// row * 32 + (gg & 1) * 16: one load instruction reads the pair's whole kilobyte). Returns the
-// lane's f64 partial; the four lanes of a row are summed by the caller.
-__device__ __forceinline__ double block_rows(const Fp4Mat m, int rb, int nkt, int G, int p0,
-                                             int p1, const uint4* act_pairs, const int* act_exp) {
-  const int lane = lane_id();
-  const int row = lane & 15, gg = lane >> 4;
-  const uint8_t* base = m.data + ((size_t)rb * nkt) * 512 + (gg >> 1) * 512 + row * 32 + (gg & 1) * 16;
-  const uint16_t* srow = m.scales + (size_t)(rb * 16 + row) * G;
-  double acc = 0.0;
-  // two pairs in flight: pair p + 1 loads while pair p is reduced
-  uint4 w0 = make_uint4(0, 0, 0, 0);
-  uint16_t s0 = 0;
-  if (p0 < p1) {
-    w0 = ld_stream(base + (size_t)p0 * 1024);
-    s0 = ld_u16(srow + 4 * p0 + gg);
-  }
-  for (int p = p0; p < p1; p++) {
-    uint4 w1 = w0;
-    uint16_t s1 = s0;
-    if (p + 1 < p1) {
-      w1 = ld_stream(base + (size_t)(p + 1) * 1024);
-      s1 = ld_u16(srow + 4 * (p + 1) + gg);
+  __device__ __forceinline__ void finish(uint4* lds_pairs, int* lds_exp) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int g = (int)threadIdx.x + r * (int)blockDim.x;
+      if (g < groups) put(lds_pairs, lds_exp, g, w[r], e[r]);
     }
-    const int g = 4 * p + gg;
-    const float sdot = group_dot(w0, act_pairs + (size_t)g * 4);
-    acc = fma((double)sdot, pow2d((int)((s0 >> 7) & 0xff) + act_exp[g] - 254), acc);
-    w0 = w1;
-    s0 = s1;
+    for (int g = (int)threadIdx.x + R * (int)blockDim.x; g < groups; g += (int)blockDim.x)
+      put(lds_pairs, lds_exp, g, *(const uint4*)(codes + (size_t)g * 16), sc[g]);
   }
-  return acc;
+};
+
+// Stream of one 16-row block of a tiled matrix over tile pairs [p0, p1): lane l owns row
+// l & 15 and, within each 1 KB pair of tiles, group (l >> 4), whose 16 bytes sit at
+// (gg >> 1) * 512 + row * 32 + (gg & 1) * 16, so one load instruction reads the pair's whole
+// kilobyte. The block's scales for the range (16 rows x ng = 4 (p1 - p0) groups, row-major in
+// memory) are read once, coalesced, two per lane-word, and kept as E8M0 bytes in LDS (se):
+// read per pair, they would cost one scattered 16-line load per kilobyte of weights.
+// D pairs are in flight; start() issues the first D before the caller stages its activations,
+// step() reduces one while issuing the next. The lane's f64 partial sum is exact.
+constexpr int kScaleRegs = 8;  // scale words per lane held across the prologue (ng <= 64)
+
+template <int D>
+struct PairStream {
+  const uint8_t* base;
+  const uint16_t* sc0;  // scale of row rb * 16 + r, group 4 p0 + j at sc0[r * G + j]
+  uint8_t* se;          // LDS [16][ng] E8M0 bytes
+  int G, ng, p0, p1, gg, row;
+  uint4 w[D];
+  uint32_t sr[kScaleRegs];
+
+  __device__ __forceinline__ void init(const Fp4Mat m, int rb, int nkt, int G_, int q0, int q1,
+                                       uint8_t* lds_e) {
+    const int lane = lane_id();
+    row = lane & 15;
+    gg = lane >> 4;
+    G = G_;
+    p0 = q0;
+    p1 = q1;
+    ng = 4 * (q1 - q0);
+    base = m.data + ((size_t)rb * nkt) * 512 + (gg >> 1) * 512 + row * 32 + (gg & 1) * 16;
+    sc0 = m.scales + (size_t)rb * 16 * G + 4 * q0;
+    se = lds_e;
+  }
+  // scale word i of the range: row i / (ng / 2), groups 2 (i % (ng / 2)) and the next
+  __device__ __forceinline__ const uint32_t* scale_word(int i) const {
+    const int h = max(ng / 2, 1), r = i / h, j = i - r * h;
+    return (const uint32_t*)(sc0 + (size_t)r * G + 2 * j);
+  }
+  __device__ __forceinline__ void issue_scales() {
+    const int n = 8 * ng;  // words: 16 rows x ng / 2
+#pragma unroll
+    for (int k = 0; k < kScaleRegs; k++) {
+      const int i = min(lane_id() + 64 * k, max(n - 1, 0));
+      sr[k] = *(const __attribute__((address_space(1))) uint32_t*)scale_word(i);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __device__ __forceinline__ void put_word(int i, uint32_t v) {
+    const int h = max(ng / 2, 1), r = i / h, j = i - r * h;
+    se[r * ng + 2 * j] = (uint8_t)(v >> 7);
+    se[r * ng + 2 * j + 1] = (uint8_t)(v >> 23);
+  }
+  __device__ __forceinline__ void finish_scales() {
+    const int n = 8 * ng;
+#pragma unroll
+    for (int k = 0; k < kScaleRegs; k++)
+      if (lane_id() + 64 * k < n) put_word(lane_id() + 64 * k, sr[k]);
+    for (int i = lane_id() + 64 * kScaleRegs; i < n; i += 64) put_word(i, *scale_word(i));
+  }
+  // pair p into buffer d (a pair past the end re-reads the last valid one: no branch around
+  // the load, so every step issues one load and the waits below stay exact)
+  __device__ __forceinline__ void issue(int d, int p) {
+    const int q = max(p < p1 ? p : p1 - 1, 0);
+    w[d] = ld_stream(base + (size_t)q * 1024);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __device__ __forceinline__ void start() {
+#pragma unroll
+    for (int d = 0; d < D; d++) issue(d, p0 + d);
+  }
+  // reduce pair p (in buffer d) into acc (p past the end: nothing) and refill the buffer with
+  // pair p + D
+  __device__ __forceinline__ void step(int d, int p, const uint4* act_pairs, const int* act_exp,
+                                       double& acc) {
+    const int pc = min(p, p1 - 1);
+    const int g = 4 * pc + gg;
+    const float sdot = group_dot(w[d], act_pairs + (size_t)g * 4);
+    const int ew = se[row * ng + 4 * (pc - p0) + gg];
+    const double t = fma((double)sdot, pow2d(ew + act_exp[g] - 254), acc);
+    acc = p < p1 ? t : acc;
+    issue(d, p + D);
+  }
+};
+
+// vmcnt(n) with the other counters left open.
+#define VIB3_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
+
+// NS streams over the same pairs (one, or up and gate of a block), interleaved: every step of
+// every stream issues one load, so before a step the loads still allowed in flight are those
+// of the NS * D - 1 steps issued after the buffer it reads.
+template <int D, int NS>
+__device__ __forceinline__ void run_streams(PairStream<D> (&st)[NS], const uint4* act_pairs,
+                                            const int* act_exp, double (&acc)[NS]) {
+#pragma unroll
+  for (int i = 0; i < NS; i++) acc[i] = 0.0;
+  const int p0 = st[0].p0, p1 = st[0].p1;
+  for (int b = p0; b < p1; b += D) {
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+#pragma unroll
+      for (int i = 0; i < NS; i++) {
+        VIB3_WAIT_VM(NS * D - 1);
+        st[i].step(d, b + d, act_pairs, act_exp, acc[i]);
+      }
+    }
+  }
 }
 
 __device__ __forceinline__ double shfl_xor_d(double v, int m) {
@@ -230,31 +337,23 @@ __device__ __forceinline__ double shfl_xor_d(double v, int m) {
 // ------------------------------------------------------------------------- kernels
 
 // Activation quantizer (kernels.cu:3193-3240): per group of 32, E8M0 from the absolute maximum,
-// values times 1/scale rounded to E2M1, packed split-half. One thread per group.
-__global__ void k_fp4_quant_act(const float* x, uint8_t* codes, uint8_t* scales, int K) {
-  const int g = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (g * 32 >= K) return;
-  float v[32];
-  float amax = 0.0f;
+// values times 1/scale rounded to E2M1, packed split-half. One lane per value: each 32-lane
+// half of a wave is one group; lane j < 16 of the group writes byte j = code j | code j+16.
+__global__ __launch_bounds__(256) void k_fp4_quant_act(const float* x, uint8_t* codes,
+                                                       uint8_t* scales, int K) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  const int lane = lane_id();
+  const float v = i < K ? x[i] : 0.0f;
+  float amax = fabsf(v);
 #pragma unroll
-  for (int i = 0; i < 32; i++) {
-    v[i] = g * 32 + i < K ? x[g * 32 + i] : 0.0f;
-    amax = fmaxf(amax, fabsf(v[i]));
-  }
+  for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
   const uint32_t e = e8m0_of_amax(amax);
   const float inv = amax == 0.0f ? 0.0f : e8m0_inv(e);
-  uint32_t w[4] = {0, 0, 0, 0};
-#pragma unroll
-  for (int j = 0; j < 16; j++) {
-    const uint32_t byte = e2m1_rne(v[j] * inv) | (e2m1_rne(v[j + 16] * inv) << 4);
-    w[j >> 2] |= byte << (8 * (j & 3));
-  }
-  if ((K & 31) == 0 || g * 32 + 32 <= K) {
-    *(uint4*)(codes + (size_t)g * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-  } else {  // a ragged last group: only its bytes
-    for (int j = 0; j < 16 && g * 32 + j < K; j++) codes[(size_t)g * 16 + j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
-  }
-  scales[g] = (uint8_t)e;
+  const uint32_t code = e2m1_rne(v * inv);
+  const uint32_t hi = (uint32_t)__shfl(code, (lane & ~31) + (lane & 15) + 16);
+  const int g = i >> 5, j = i & 31;
+  if (j < 16 && g * 32 + j < K) codes[(size_t)g * 16 + j] = (uint8_t)(code | (hi << 4));
+  if (j == 0 && g * 32 < K) scales[g] = (uint8_t)e;
 }
 
 // Gate/up of every active expert + SwiGLU + FP4 quantization of h (kernels.cu:5357-5517 fused):
@@ -280,12 +379,28 @@ __global__ __launch_bounds__(512) void k_fp4_gateup(Fp4Args a) {
     if (threadIdx.x == 0) hsc[q] = 0;
     return;
   }
-  stage_groups(a.act, a.act_sc, Gin, act_pairs, act_exp);
-  __syncthreads();
   const int rb = 2 * q + (wave >> 2), kq = wave & 3;
   const int p0 = kq * P / 4, p1 = (kq + 1) * P / 4;
-  double u = block_rows(up, rb, nkt, Gin, p0, p1, act_pairs, act_exp);
-  double g = block_rows(gate, rb, nkt, Gin, p0, p1, act_pairs, act_exp);
+  const int ngmax = 4 * ((P + 3) / 4);
+  uint8_t* se = (uint8_t*)(act_exp + Gin) + (size_t)wave * 2 * 16 * ngmax;
+  // staging and scale loads first, then the first weight loads, then the conversions (which
+  // wait only for the staging and scale loads)
+  Stage<2> stage;
+  stage.issue(a.act, a.act_sc, Gin);
+  PairStream<kFp4Depth> st[2];
+  st[0].init(up, rb, nkt, Gin, p0, p1, se);
+  st[1].init(gate, rb, nkt, Gin, p0, p1, se + 16 * ngmax);
+  st[0].issue_scales();
+  st[1].issue_scales();
+  st[0].start();  // unconditional (an empty range re-reads pair 0): the waits stay exact
+  st[1].start();
+  stage.finish(act_pairs, act_exp);
+  st[0].finish_scales();
+  st[1].finish_scales();
+  __syncthreads();
+  double acc[2] = {0.0, 0.0};
+  if (p0 < p1) run_streams<kFp4Depth, 2>(st, act_pairs, act_exp, acc);
+  double u = acc[0], g = acc[1];
   u += shfl_xor_d(u, 16);
   g += shfl_xor_d(g, 16);
   u += shfl_xor_d(u, 32);
@@ -330,24 +445,53 @@ __global__ __launch_bounds__(512) void k_fp4_down(Fp4Args a) {
   const int rb = (int)blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = lane_id();
-  for (int s = 0; s < a.n; s++) {
-    const uint8_t* hc = a.mid + (size_t)s * a.mid_stride;
-    stage_groups(hc, hc + a.M_mid / 2, Gm, hp + (size_t)s * Gm * 4, he + (size_t)s * Gm);
-  }
-  __syncthreads();
   const int s = wave;
-  float ds = 0.0f;
-  bool use = false;
-  if (s < a.n) {
-    const Fp4Mat dn = slot_mat(a, s, 2, a.M_out, a.M_mid);
-    use = dn.data && dn.scales;
-    if (use) {
-      double acc = block_rows(dn, rb, nkt, Gm, 0, P, hp + (size_t)s * Gm * 4, he + (size_t)s * Gm);
-      acc += shfl_xor_d(acc, 16);
-      acc += shfl_xor_d(acc, 32);
-      ds = (float)acc;
+  const Fp4Mat dn = s < a.n ? slot_mat(a, s, 2, a.M_out, a.M_mid) : Fp4Mat{nullptr, nullptr};
+  const bool use = dn.data && dn.scales;
+  Stage<1> stage;  // this workgroup's share of every slot's intermediate: one group per thread
+  const int ng = a.n * Gm;
+  {
+    // thread t stages group t of the flattened [slot][group] list (slot stride mid_stride)
+    const int t = min((int)threadIdx.x, ng - 1), sl = t / Gm, gi = t - sl * Gm;
+    const uint8_t* hc = a.mid + (size_t)sl * a.mid_stride;
+    stage.w[0] = *(const uint4*)(hc + (size_t)gi * 16);
+    stage.e[0] = hc[a.M_mid / 2 + gi];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  PairStream<kFp4Depth> sd[1];
+  // the scale and first weight loads go out behind the staging loads, unconditionally (an
+  // unusable slot streams one pair of the intermediate buffer instead, never used)
+  uint8_t* se = (uint8_t*)(he + (size_t)a.n * Gm) + (size_t)wave * 16 * Gm;
+  sd[0].init(use ? dn : Fp4Mat{a.mid, (const uint16_t*)a.mid}, use ? rb : 0, nkt, use ? Gm : 0,
+             0, use ? P : 1, se);
+  sd[0].issue_scales();
+  sd[0].start();
+  for (int t = (int)threadIdx.x; t < ng; t += (int)blockDim.x) {
+    const int sl = t / Gm, gi = t - sl * Gm;
+    uint4 w;
+    uint8_t e;
+    if (t == (int)threadIdx.x) {
+      w = stage.w[0];
+      e = stage.e[0];
+    } else {
+      const uint8_t* hc = a.mid + (size_t)sl * a.mid_stride;
+      w = *(const uint4*)(hc + (size_t)gi * 16);
+      e = hc[a.M_mid / 2 + gi];
     }
-    if (lane < 16) d[s][lane] = use ? ds : 0.0f;
+    Stage<1>::put(hp + (size_t)sl * Gm * 4, he + (size_t)sl * Gm, gi, w, e);
+  }
+  sd[0].finish_scales();
+  __syncthreads();
+  if (s < a.n) {
+    float ds = 0.0f;
+    if (use) {
+      double acc[1];
+      run_streams<kFp4Depth, 1>(sd, hp + (size_t)s * Gm * 4, he + (size_t)s * Gm, acc);
+      acc[0] += shfl_xor_d(acc[0], 16);
+      acc[0] += shfl_xor_d(acc[0], 32);
+      ds = (float)acc[0];
+    }
+    if (lane < 16) d[s][lane] = ds;
   }
   __syncthreads();
   if (threadIdx.x < 16) {
@@ -426,14 +570,24 @@ int current_device() {
   return dev;
 }
 
+// LDS of the two kernels: decoded activation / intermediate groups (64 + 4 bytes each) plus
+// each wave's E8M0 bytes of its block's scales.
+size_t gateup_lds(int K_in) {
+  const int Gin = K_in / 32, P = K_in / 128;
+  return (size_t)Gin * 68 + (size_t)8 * 2 * 16 * (4 * ((P + 3) / 4));
+}
+size_t down_lds(int n, int M_mid) {
+  const int Gm = M_mid / 32;
+  return (size_t)n * Gm * 68 + (size_t)n * 16 * Gm;
+}
+
 // Shape limits of the fused kernels: tiles of 16 rows x 64 columns taken in 128-column pairs,
-// 32-row E8M0 groups of h, decoded activations / intermediates within 64 KB of LDS.
+// 32-row E8M0 groups of h, each kernel's LDS within 64 KB.
 int check_shape(int n, int K_in, int M_mid, int K_mid, int M_out) {
   if (n <= 0 || n > kFp4MaxActive) return VIB3_ERR_BAD_COUNT;  // kernels.cu:5672
   if (K_in <= 0 || M_mid <= 0 || M_out <= 0 || K_mid != M_mid) return VIB3_ERR_BAD_COUNT;
   if (K_in % 128 || M_mid % 128 || M_out % 16) return VIB3_ERR_UNSUPPORTED;
-  if ((size_t)K_in * 2 + K_in / 8 > 65536) return VIB3_ERR_UNSUPPORTED;
-  if ((size_t)n * M_mid * 2 + (size_t)n * M_mid / 8 > 65536) return VIB3_ERR_UNSUPPORTED;
+  if (gateup_lds(K_in) > 65536 || down_lds(n, M_mid) > 65536) return VIB3_ERR_UNSUPPORTED;
   return 0;
 }
 
@@ -444,11 +598,10 @@ int launch_fused(Fp4Args& a, hipStream_t st) {
   if (!mb.ptr || mb.max_mid < a.M_mid) return VIB3_ERR_WORKSPACE;  // not prewarmed
   a.mid = mb.ptr;
   a.mid_stride = mb.stride;
-  const int Gin = a.K_in / 32, Gm = a.M_mid / 32;
   hipLaunchKernelGGL(k_fp4_gateup, dim3((unsigned)(a.M_mid / 32), (unsigned)a.n), dim3(512),
-                     (unsigned)((size_t)Gin * 64 + (size_t)Gin * 4), st, a);
+                     (unsigned)gateup_lds(a.K_in), st, a);
   hipLaunchKernelGGL(k_fp4_down, dim3((unsigned)(a.M_out / 16)), dim3(64 * a.n),
-                     (unsigned)((size_t)a.n * Gm * 64 + (size_t)a.n * Gm * 4), st, a);
+                     (unsigned)down_lds(a.n, a.M_mid), st, a);
   VIB3_RETURN_LAUNCH();
 }
 
@@ -465,7 +618,7 @@ int vib3_launch_quantize_activation_fp4(const void* input, void* act_fp4, void* 
   if (!input || !act_fp4 || !act_scales) return VIB3_ERR_BAD_POINTER;
   if (((uintptr_t)act_fp4 & 15)) return VIB3_ERR_BAD_POINTER;
   const int groups = (K + 31) / 32;
-  hipLaunchKernelGGL(k_fp4_quant_act, dim3((unsigned)((groups + 63) / 64)), dim3(64), 0,
+  hipLaunchKernelGGL(k_fp4_quant_act, dim3((unsigned)((groups * 32 + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, (const float*)input, (uint8_t*)act_fp4,
                      (uint8_t*)act_scales, K);
   VIB3_RETURN_LAUNCH();
