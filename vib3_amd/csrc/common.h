@@ -254,9 +254,10 @@ __device__ __forceinline__ void mat_row(const MatRef& m, int r, int pk, int ng, 
 }  // namespace vib3
 
 // Timeline probes for kernel-internal phases: compiled in only when VIB3_TRACE is defined (a
-// profiling build that also defines `uint64_t* vib3_trace_buf` in device memory); each probe
-// stores the 100 MHz real-time counter for (workgroup, point).
+// profiling build; the buffer pointer is set per translation unit by vib3_trace_set in
+// int4_gemv.hip); each probe stores the 100 MHz real-time counter for (workgroup, point).
 #ifdef VIB3_TRACE
+static __device__ uint64_t* vib3_trace_buf;
 #define VIB3_TRACE_POINT(k)                                                          \
   do {                                                                               \
     if (threadIdx.x == 0) vib3_trace_buf[blockIdx.x * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); \

@@ -269,7 +269,6 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // pipeline serves the router rows, which every routed row waits for, first. (Cutting rows
   // into halves to spread them evenly over the two workgroups of a CU measured slower.)
   const bool fused = PAGED && a.route == kRouteFused;
-  if (fused && a.router.gen_word) a.router.gen = next_tag(*a.router.gen_word);
   const int E = a.router.E, G = (int)gridDim.x;
   auto publish = [&](int e, float v) {
     if (threadIdx.x == 0) {
@@ -282,12 +281,16 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   const bool split_row = fused && (int)blockIdx.x < E && router_seg_ok(a.router, 1, 4);
   RouterSegRaw<4> rrow;
   if (split_row) router_seg_issue<4>(a.router, (int)blockIdx.x, 0, 1, rrow);
+  VIB3_TRACE_POINT(11);  // router row issued
+  // this launch's tag, read once the router row's loads are out
+  if (fused && a.router.gen_word) a.router.gen = next_tag(*a.router.gen_word);
   const bool early_now = early && !(fused && (int)blockIdx.x < E);
   if (early_now) start(buf[0], 0, true, it0);
   if (fused) {
     int e = (int)blockIdx.x;
     if (split_row) {
       publish(e, router_seg_finish<4>(a.router, 1, rrow));
+      VIB3_TRACE_POINT(12);  // router row published
       e += G;
     }
     for (; e < E; e += G) {  // more rows than workgroups: one at a time
@@ -1031,3 +1034,12 @@ int launch_generic(GenericArgs a, bool dual, hipStream_t s) {
 }
 
 }  // namespace vib3
+
+#ifdef VIB3_TRACE
+// Profiling builds only: where this translation unit's kernels write their timeline probes
+// (16 u64 per workgroup).
+extern "C" int vib3_trace_set(void* buf) {
+  uint64_t* p = (uint64_t*)buf;
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(vib3_trace_buf), &p, sizeof(p));
+}
+#endif
