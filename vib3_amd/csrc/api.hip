@@ -464,6 +464,7 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only,
   a.out = ws + w.h; a.out_dt = h_dt; a.out_stride = (size_t)L->inter;
   a.route = route;
   a.router = router;
+  a.x_i16 = getenv("VIB3_F32_SPLIT") ? 0 : 1;  // f32 stream: int16 chunks (A/B knob: split)
   if (run(1)) {
     int rc = launch_rows(a, true, st);
     if (rc) return rc;

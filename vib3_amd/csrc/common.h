@@ -151,6 +151,60 @@ __device__ __forceinline__ bool make_chunk(const float* xv, XChunk& hi, XChunk& 
   return need;
 }
 
+// Activation modes of the INT4 row kernels: f16 pairs (exact for f16 / bf16 activations),
+// f32 split into hi + lo f16 pairs (two dot products per pair), or f32 as int16 block fixed
+// point per 32-element chunk (one integer dot product per pair).
+enum { kXf16 = 0, kXsplit = 1, kXi16 = 2 };
+
+// Chunk of 32 f32 activations as int16 pairs x_i = rint(x * 2^sh), sh = 15 - E with E the
+// exponent of the chunk's largest |x| (|x_i| <= 32767), in the slots of hi (the pair layout
+// of chunk_dot); hi.xs8 = the bits of 8 * sum(x_i) as an int, lo.xs8 = 2^(-sh-24), the factor
+// that brings the integer dot back to chunk_dot's 2^-24 units. Error per element at most half
+// a unit of 2^-sh: 2^-16 of the chunk's largest value.
+__device__ __forceinline__ void make_chunk_i16(const float* xv, XChunk& hi, XChunk& lo) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; j++) amax = fmaxf(amax, __builtin_fabsf(xv[j]));
+  int E = 0;
+  (void)__builtin_frexpf(amax, &E);  // amax = f 2^E, f in [0.5, 1)
+  const int sh = amax > 0.0f ? 15 - E : 0;
+  int sum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    int q[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float t = __builtin_rintf(__builtin_ldexpf(xv[8 * i + j], sh));
+      q[j] = (int)fminf(fmaxf(t, -32767.0f), 32767.0f);
+      sum += q[j];
+    }
+    auto pk = [](int a, int b) { return as_h2(((uint32_t)a & 0xffffu) | ((uint32_t)b << 16)); };
+    hi.a[i] = pk(q[0], q[4]);
+    hi.b[i] = pk(q[1], q[5]);
+    hi.c[i] = pk(q[2], q[6]);
+    hi.d[i] = pk(q[3], q[7]);
+  }
+  hi.xs8 = __int_as_float(8 * sum);
+  lo.xs8 = __builtin_ldexpf(1.0f, -sh - 24);
+}
+
+typedef short s2 __attribute__((ext_vector_type(2)));
+
+// chunk_dot for an int16 chunk: sum (q - 8) x_i exactly in integers, times 2^(-sh-24).
+__device__ __forceinline__ float chunk_dot_i16(const uint4 w, const XChunk& x, float mult) {
+  const uint32_t v[4] = {w.x, w.y, w.z, w.w};
+  int c1 = 0, c2 = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t u = v[i], t = v[i] >> 8;
+    c1 = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, u & 0x000F000Fu), __builtin_bit_cast(s2, x.a[i]), c1, false);
+    c2 = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, u & 0x00F000F0u), __builtin_bit_cast(s2, x.b[i]), c2, false);
+    c1 = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, t & 0x000F000Fu), __builtin_bit_cast(s2, x.c[i]), c1, false);
+    c2 = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, t & 0x00F000F0u), __builtin_bit_cast(s2, x.d[i]), c2, false);
+  }
+  return (float)(c1 + (c2 >> 4) - __float_as_int(x.xs8)) * mult;
+}
+
 __device__ __forceinline__ void zero_chunk(XChunk& c) {
 #pragma unroll
   for (int i = 0; i < 4; i++) c.a[i] = c.b[i] = c.c[i] = c.d[i] = h2{(half_t)0, (half_t)0};

@@ -77,7 +77,7 @@ __device__ __forceinline__ void issue(RowBatch<NCH, DUAL, U>& b, const MatRef& m
 }
 
 // Wave-uniform sums (scaled back by 2^24) of the batch's rows.
-template <int NCH, bool DUAL, bool SPLIT, int U>
+template <int NCH, bool DUAL, int XM, int U>
 __device__ __forceinline__ void reduce(const RowBatch<NCH, DUAL, U>& b, const XChunk (&xh)[NCH],
                                        const XChunk (&xl)[NCH], const int (&cidx)[NCH], int cpr,
                                        int sdt, float (&t0)[U], float (&t1)[U]) {
@@ -86,12 +86,14 @@ __device__ __forceinline__ void reduce(const RowBatch<NCH, DUAL, U>& b, const XC
     float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
-      float p0 = chunk_dot(b.w0[u][j], xh[j]);
-      if (SPLIT) p0 += chunk_dot(b.w0[u][j], xl[j]);
+      float p0 = XM == kXi16 ? chunk_dot_i16(b.w0[u][j], xh[j], xl[j].xs8)
+                             : chunk_dot(b.w0[u][j], xh[j]);
+      if (XM == kXsplit) p0 += chunk_dot(b.w0[u][j], xl[j]);
       acc0 = __builtin_fmaf(p0, decode_scale(b.q0[u][j], sdt), acc0);
       if (DUAL) {
-        float p1 = chunk_dot(b.w1[u][j], xh[j]);
-        if (SPLIT) p1 += chunk_dot(b.w1[u][j], xl[j]);
+        float p1 = XM == kXi16 ? chunk_dot_i16(b.w1[u][j], xh[j], xl[j].xs8)
+                               : chunk_dot(b.w1[u][j], xh[j]);
+        if (XM == kXsplit) p1 += chunk_dot(b.w1[u][j], xl[j]);
         acc1 = __builtin_fmaf(p1, decode_scale(b.q1[u][j], sdt), acc1);
       }
     }
@@ -100,14 +102,14 @@ __device__ __forceinline__ void reduce(const RowBatch<NCH, DUAL, U>& b, const XC
   }
 }
 
-template <bool PAGED, int NCH, bool DUAL, bool SPLIT, int U>
+template <bool PAGED, int NCH, bool DUAL, int XM, int U>
 __device__ __forceinline__ void dot_rows(const MatRef& m0, const MatRef& m1, const int (&ra)[U],
                                          const XChunk (&xh)[NCH], const XChunk (&xl)[NCH],
                                          const int (&cidx)[NCH], const int (&gidx)[NCH], int pk,
                                          int ng, int cpr, int sdt, float (&t0)[U], float (&t1)[U]) {
   RowBatch<NCH, DUAL, U> b;
   issue<PAGED, NCH, DUAL, U>(b, m0, m1, ra, cidx, gidx, pk, ng, cpr);
-  reduce<NCH, DUAL, SPLIT, U>(b, xh, xl, cidx, cpr, sdt, t0, t1);
+  reduce<NCH, DUAL, XM, U>(b, xh, xl, cidx, cpr, sdt, t0, t1);
 }
 
 // Chunk indices of this lane: chunk c = (ks * NCH + j) * 64 + lane and its scale group.
@@ -123,7 +125,7 @@ __device__ __forceinline__ void chunk_index(int ks, int g, int cpr, int (&cidx)[
 }
 
 // Activation chunks of this lane (see chunk_index), converted to f16 pairs.
-template <int NCH, bool SPLIT>
+template <int NCH, int XM>
 __device__ __forceinline__ void load_x(const void* x, int x_dt, int cpr, const int (&cidx)[NCH],
                                        XChunk (&xh)[NCH], XChunk (&xl)[NCH]) {
 #pragma unroll
@@ -131,8 +133,12 @@ __device__ __forceinline__ void load_x(const void* x, int x_dt, int cpr, const i
     if (cidx[j] < cpr) {
       float xv[32];
       load_chunk_act(x, x_dt, cidx[j], xv);
-      make_chunk(xv, xh[j], xl[j]);
-      if (!SPLIT) zero_chunk(xl[j]);
+      if (XM == kXi16) {
+        make_chunk_i16(xv, xh[j], xl[j]);
+      } else {
+        make_chunk(xv, xh[j], xl[j]);
+        if (XM != kXsplit) zero_chunk(xl[j]);
+      }
     } else {
       zero_chunk(xh[j]);
       zero_chunk(xl[j]);
@@ -168,7 +174,7 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, size_t o, float v) 
 // KS > 1: the KS waves of a team split one row's k range and combine through LDS.
 
 
-template <int NCH, bool DUAL, bool SPLIT, bool PAGED>
+template <int NCH, bool DUAL, int XM, bool PAGED>
 __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   VIB3_TRACE_POINT(0);
   const int lane = lane_id();
@@ -251,7 +257,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   int kres = 0;
   auto finish = [&](const RowBatch<NCH, DUAL, 1>& buf) {
     float t0[1], t1[1];
-    reduce<NCH, DUAL, SPLIT, 1>(buf, xh, xl, cidx, cpr, a.sdt, t0, t1);
+    reduce<NCH, DUAL, XM, 1>(buf, xh, xl, cidx, cpr, a.sdt, t0, t1);
     const float v = rows_epilogue(DUAL, t0[0], t1[0]);
     if (lane == kres) res = v;
     kres++;
@@ -301,7 +307,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // the activations, while the routing is pending; the selecting wave of a launch without
   // fused routing selects first (its loads would queue behind its early batch)
   const bool sel_first = wave == 0 && !fused;
-  if (!sel_first) load_x<NCH, SPLIT>(a.x, a.x_dt, cpr, cidx, xh, xl);
+  if (!sel_first) load_x<NCH, XM>(a.x, a.x_dt, cpr, cidx, xh, xl);
   VIB3_TRACE_POINT(1);
   if (PAGED && top_k > 0 && wave == 0) {
     // the selection is on every routed row's critical path: issue ahead of the streaming
@@ -324,7 +330,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     __builtin_amdgcn_s_setprio(0);
     VIB3_TRACE_POINT(2);
   }
-  if (sel_first) load_x<NCH, SPLIT>(a.x, a.x_dt, cpr, cidx, xh, xl);
+  if (sel_first) load_x<NCH, XM>(a.x, a.x_dt, cpr, cidx, xh, xl);
   __syncthreads();
   VIB3_TRACE_POINT(3);
   if (!have) return;
@@ -369,7 +375,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   VIB3_TRACE_POINT(4);
 }
 
-template <int NCH, bool DUAL, bool SPLIT, bool PAGED>
+template <int NCH, bool DUAL, int XM, bool PAGED>
 __global__ __launch_bounds__(256) void k_int4_rows_ksplit(RowsArgs a) {
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform (SGPR)
@@ -387,12 +393,12 @@ __global__ __launch_bounds__(256) void k_int4_rows_ksplit(RowsArgs a) {
   const MatRef m0 = slot_matrix(a, slot, e, 0, 0);
   const MatRef m1 = DUAL ? slot_matrix(a, slot, e, 1, 1) : m0;
   chunk_index<NCH>(ks, a.g, cpr, cidx, gidx);
-  load_x<NCH, SPLIT>(a.x, a.x_dt, cpr, cidx, xh, xl);
+  load_x<NCH, XM>(a.x, a.x_dt, cpr, cidx, xh, xl);
   float res0 = 0.f, res1 = 0.f;
   for (int i = 0; i < nrows; i += 2) {
     const int ra[2] = {r0 + i, i + 1 < nrows ? r0 + i + 1 : r0 + i};
     float t0[2], t1[2];
-    dot_rows<PAGED, NCH, DUAL, SPLIT, 2>(m0, m1, ra, xh, xl, cidx, gidx, pk, ng, cpr, a.sdt, t0, t1);
+    dot_rows<PAGED, NCH, DUAL, XM, 2>(m0, m1, ra, xh, xl, cidx, gidx, pk, ng, cpr, a.sdt, t0, t1);
     if (lane == i) { res0 = t0[0]; res1 = t1[0]; }
     if (lane == i + 1) { res0 = t0[1]; res1 = t1[1]; }
   }
@@ -889,7 +895,7 @@ static int env_int(const char* name, int dflt) {
   return v && atoi(v) > 0 ? atoi(v) : dflt;
 }
 
-template <int N, bool D, bool S, bool P>
+template <int N, bool D, int S, bool P>
 static void launch_rows_p(RowsArgs& a, hipStream_t s, KTime t) {
   if (a.KS == 1) {
     auto k = k_int4_rows<N, D, S, P>;
@@ -911,8 +917,9 @@ static void launch_rows_p(RowsArgs& a, hipStream_t s, KTime t) {
 }
 
 
-template <int N, bool D, bool S>
+template <int N, bool D, int S>
 static void launch_rows_t(RowsArgs& a, hipStream_t s, KTime t) {
+  if (S == kXi16) return launch_rows_p<N, D, kXi16, true>(a, s, t);  // paged launches only
   if (!a.routed_table) return launch_rows_p<N, D, S, false>(a, s, t);
   return launch_rows_p<N, D, S, true>(a, s, t);
 }
@@ -923,11 +930,15 @@ int launch_rows(RowsArgs a, bool dual, hipStream_t s, KTime t) {
   a.KS = ks;
   if (a.RPT <= 0 || a.RPT > kWave) a.RPT = 8;
   if (a.M <= 0 || a.nslots <= 0) return 0;
-  const bool split = a.x_dt == VIB3_DT_F32;
+  // f32 activations: int16 block fixed point where the caller asks for it (paged layer
+  // launches with k in one pass), else the hi + lo f16 split
+  const int xm = a.x_dt != VIB3_DT_F32 ? kXf16
+                 : (a.x_i16 && a.routed_table && ks == 1) ? kXi16 : kXsplit;
 #define VIB3_ROWS(N, D)                                   \
   do {                                                    \
-    if (split) launch_rows_t<N, D, true>(a, s, t);        \
-    else launch_rows_t<N, D, false>(a, s, t);             \
+    if (xm == kXi16) launch_rows_t<N, D, kXi16>(a, s, t); \
+    else if (xm == kXsplit) launch_rows_t<N, D, kXsplit>(a, s, t); \
+    else launch_rows_t<N, D, kXf16>(a, s, t);             \
   } while (0)
   if (dual) {
     if (nch == 1) VIB3_ROWS(1, true);

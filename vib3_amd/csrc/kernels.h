@@ -87,6 +87,9 @@ struct RowsArgs {
   // takes experts b, b + grid, ...), publish them as tagged slots, and then select as above.
   int route;
   RouterArgs router;
+  // f32 activations of a paged launch as int16 block fixed point (one integer dot product per
+  // weight pair, error 2^-16 of each 32-chunk's largest value) instead of the hi + lo split
+  int x_i16;
 };
 
 // Down projection of every slot for a block of RB output rows plus the weighted expert sum.
