@@ -77,11 +77,46 @@ def algorithmic_bytes(cfg, shape) -> dict:
     }
 
 
+def host_cpu() -> dict:
+    """The CPU the baseline runs on: model, logical CPUs, the CPUs this process may use, and
+    the threads the baseline uses (this pool gives each GPU's process a 16-CPU share)."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
+                         None)
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or affinity
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity": affinity,
+            "threads": max(1, min(affinity, share))}
+
+
+def median_time(fn, budget_s: float, min_reps: int = 3, max_reps: int = 200):
+    """Median wall time of fn() over about budget_s seconds (after one warm-up call)."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < min_reps:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= max_reps:
+            break
+    return statistics.median(times), len(times)
+
+
 def cpu_baseline(cfg, bank, w, b, x, ids, wts, budget_s: float):
-    """Time the oracle (C restatement of vib3's CPU fallback) on the same layer and token."""
+    """Time the oracle (C restatement of vib3's CPU fallback) on the same layer and token, with
+    every thread of the process's CPU share and with one thread."""
     import numpy as np
     from oracle import oracle as O
-    threads = min(16, os.cpu_count() or 1)
+    host = host_cpu()
+    threads = host["threads"]
     xh = x.float().cpu().numpy()
     wh = w.cpu().numpy()
     bh = b.cpu().numpy() if b is not None else None
@@ -90,27 +125,21 @@ def cpu_baseline(cfg, bank, w, b, x, ids, wts, budget_s: float):
     shared = [bank.expert_pages_host(cfg["E"] + s) for s in range(cfg["shared"])]
     sdt = O.BF16 if cfg["sdt"] == "bf16" else O.F16
 
-    def one():
+    def one(n):
         r_ids, r_wts, _ = O.router(xh, wh, O.F32, cfg["E"], cfg["hidden"], cfg["k"], cfg["mode"],
-                                   cfg["scaling"], True, bh, nthreads=threads)
+                                   cfg["scaling"], True, bh, nthreads=n)
         O.moe_layer(xh, cfg["hidden"], cfg["inter"], cfg["g"], sdt, routed, r_ids, r_wts, shared,
-                    faithful=True, nthreads=threads)
+                    faithful=True, nthreads=n)
 
-    one()  # warm-up (page the copied weights in)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        one()
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 200:
-            break
-    med = statistics.median(times)
+    med, reps = median_time(lambda: one(threads), budget_s)
+    med1, reps1 = median_time(lambda: one(1), budget_s / 2, min_reps=3, max_reps=50)
     return {"value": med * 1e6, "unit": "us/layer", "cores": threads, "kind": "port",
+            "single_thread_us": round(med1 * 1e6, 1), "host": host,
             "sample": f"c-oracle restatement of kernels.rs CPU fallback (router + "
                       f"{cfg['k']}+{cfg['shared']} experts, f16 rounding points kept) on the same "
-                      f"layer/token as the GPU; median of {len(times)} reps, {threads} threads",
-            "reps": len(times)}
+                      f"layer/token as the GPU; median of {reps} reps with {threads} threads (the "
+                      f"process's CPU share), median of {reps1} reps with 1 thread",
+            "reps": reps}
 
 
 def bench_c4(args, cfg) -> int:
@@ -173,27 +202,29 @@ def bench_c4(args, cfg) -> int:
     if not args.no_cpu:
         from oracle import oracle as O
         ids, w = picks[0]
-        sample = [0, 1]
         xh = O.to_f32(xs[0].view(torch.int16).cpu().numpy().view(np.uint16).ravel(),
                       O.BF16).reshape(T, H)
-        used = sorted({int(e) for e in ids[sample].ravel()})
+        used = sorted({int(e) for e in ids.ravel()})
         empty = np.zeros(1, dtype=np.uint8)
         pages = [banks[0].expert_pages_host(e) if e in used else (empty, empty, empty)
                  for e in range(E)]
-        threads = min(16, os.cpu_count() or 1)
-        O.moe_mxfp4_batched(xh[sample], H, I, pages, ids[sample], w[sample], nthreads=threads)
-        times = []
-        t_end = time.perf_counter() + args.cpu_seconds
-        while time.perf_counter() < t_end or len(times) < 2:
-            c0 = time.perf_counter()
-            O.moe_mxfp4_batched(xh[sample], H, I, pages, ids[sample], w[sample], nthreads=threads)
-            times.append(time.perf_counter() - c0)
-        per_tok = statistics.median(times) / len(sample)
-        cpu = {"value": round(per_tok * T * 1e6, 1), "unit": "us/batch", "cores": threads,
-               "kind": "port",
-               "sample": f"c-oracle per-token restatement on {len(sample)} tokens of batch 0 "
-                         f"(8 experts each), median of {len(times)} reps, scaled x{T // len(sample)} "
-                         f"to the 64-token batch"}
+        host = host_cpu()
+        threads = host["threads"]
+        # the whole 64-token batch 0 with the process's CPU share (one warm-up, then timed runs
+        # within the budget, at least one)
+        full, reps = median_time(
+            lambda: O.moe_mxfp4_batched(xh, H, I, pages, ids, w, nthreads=threads),
+            args.cpu_seconds, min_reps=1, max_reps=5)
+        # one thread: token 0 alone, stated as such
+        one, reps1 = median_time(
+            lambda: O.moe_mxfp4_batched(xh[:1], H, I, pages, ids[:1], w[:1], nthreads=1),
+            args.cpu_seconds / 2, min_reps=2, max_reps=20)
+        cpu = {"value": round(full * 1e6, 1), "unit": "us/batch", "cores": threads,
+               "kind": "port", "host": host,
+               "single_thread_us_per_token": round(one * 1e6, 1),
+               "sample": f"c-oracle per-token restatement over all {T} tokens of batch 0 "
+                         f"(8 experts each, {len(used)} distinct), median of {reps} runs with "
+                         f"{threads} threads; single thread: token 0, median of {reps1} runs"}
 
     traffic = None  # HBM bytes per batch of the two GEMM launches, from the committed PMC summary
     tpath = os.path.join(ROOT, "profiles", "traffic_c4.json")
