@@ -83,9 +83,11 @@ __global__ void k_zero(uint4* p16, size_t n16, uint8_t* tail, size_t ntail) {
 }
 
 // Workspace of the fused layer: [scores[E] | ids[k] | wts[k] | router slots u64[E] |
-// status: error i32, router tag u32 | h[nslots][inter] | xn f32[hidden] (with a norm) | shared weights f32[num_shared] (gated)].
+// status: error i32, router tag u32 | h[nslots][inter] | xn f32[hidden] (with a norm) |
+// shared weights f32[num_shared] (gated) | down page addresses u64[nslots][down pages]].
 struct LayerWs {
-  size_t scores, ids, wts, slots, error, h, xn, shared_w, total;
+  size_t scores, ids, wts, slots, error, h, xn, shared_w, dbase, total;
+  int down_pages;  // pages of one down matrix (whole layer launches of a paged layer)
 };
 
 // The no-allocation entry point's device memory: the layer workspace of
@@ -157,7 +159,10 @@ LayerWs layer_ws(const vib3_moe_int4_layer* L, bool scratch = false) {
   w.h = next;
   w.xn = round_up(w.h + hsz * (size_t)(nslots > 0 ? nslots : 0) * (size_t)(L->inter > 0 ? L->inter : 0), 256);
   w.shared_w = round_up(w.xn + (L->norm_weight ? 4 * (size_t)(L->hidden > 0 ? L->hidden : 0) : 0), 256);
-  w.total = round_up(w.shared_w + (L->shared_gate ? 4 * (size_t)(L->num_shared > 0 ? L->num_shared : 0) : 0), 256);
+  w.dbase = round_up(w.shared_w + (L->shared_gate ? 4 * (size_t)(L->num_shared > 0 ? L->num_shared : 0) : 0), 256);
+  const int rpp = L->rows_per_page[2];
+  w.down_pages = rpp > 0 && L->hidden > 0 ? (L->hidden + rpp - 1) / rpp : 0;
+  w.total = round_up(w.dbase + 8 * (size_t)(nslots > 0 ? nslots : 0) * (size_t)w.down_pages, 256);
   return w;
 }
 
@@ -465,6 +470,13 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only,
   a.route = route;
   a.router = router;
   a.x_i16 = getenv("VIB3_F32_SPLIT") ? 0 : 1;  // f32 stream: int16 chunks (A/B knob: split)
+  // the gate/up kernel lists the down page addresses for the down kernel (a down stage alone
+  // reads the list its gate/up stage left, like h and the ids)
+  const bool bases = w.down_pages > 0 && w.down_pages <= L->max_pages && rows_write_bases(a);
+  if (bases) {
+    a.down_bases = (uint64_t*)(ws + w.dbase);
+    a.down_pages = w.down_pages;
+  }
   if (run(1)) {
     int rc = launch_rows(a, true, st);
     if (rc) return rc;
@@ -476,6 +488,10 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only,
   d.shared_table = L->shared_page_table; d.ids = ids; d.wts = wts; d.top_k = L->top_k;
   d.max_pages = L->max_pages; d.rpp = L->rows_per_page[2];
   d.magic = page_magic(L->rows_per_page[2]);
+  if (bases) {
+    d.bases = (const uint64_t*)(ws + w.dbase);
+    d.bases_stride = w.down_pages;
+  }
   d.round_f16 = (L->flags & VIB3_MOE_F32_INTERMEDIATE) ? 0 : 1;
   d.out = L->out;
   d.residual = L->residual;

@@ -307,6 +307,10 @@ __device__ __forceinline__ void mat_row(const MatRef& m, int r, int pk, int ng, 
 
 }  // namespace vib3
 
+// s_waitcnt for at most n vector-memory operations outstanding (n < 64; lgkm and exp counts
+// left at their maximum)
+#define VIB3_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
+
 // Timeline probes for kernel-internal phases: compiled in only when VIB3_TRACE is defined (a
 // profiling build; the buffer pointer is set per translation unit by vib3_trace_set in
 // int4_gemv.hip); each probe stores the 100 MHz real-time counter for (workgroup, point).

@@ -304,9 +304,6 @@ struct PairStream {
   }
 };
 
-// vmcnt(n) with the other counters left open.
-#define VIB3_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
-
 // NS streams over the same pairs (one, or up and gate of a block), interleaved: every step of
 // every stream issues one load, so before a step the loads still allowed in flight are those
 // of the NS * D - 1 steps issued after the buffer it reads.

@@ -333,6 +333,18 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   if (sel_first) load_x<NCH, XM>(a.x, a.x_dt, cpr, cidx, xh, xl);
   __syncthreads();
   VIB3_TRACE_POINT(3);
+  // block 0's first wave: the down segment's page addresses of every slot, for the down
+  // kernel (one table round trip there less)
+  if (PAGED && a.down_bases && blockIdx.x == 0 && wave == 0) {
+    typedef __attribute__((address_space(1))) const uint64_t gtab;
+    for (int i = lane; i < a.nslots * a.down_pages; i += kWave) {
+      const int sl = i / a.down_pages, p = i - sl * a.down_pages;
+      const uint64_t* t =
+          sl < top_k ? a.routed_table + ((size_t)s_sel[sl] * 3 + 2) * a.max_pages
+                     : a.shared_table + ((size_t)(sl - top_k) * 3 + 2) * a.max_pages;
+      a.down_bases[i] = *(gtab*)(t + p);
+    }
+  }
   if (!have) return;
   if (PAGED) {
     // lane k <- this wave's k-th item (lanes past the end keep a valid page-table row)
@@ -612,6 +624,11 @@ __device__ __forceinline__ float lanes_sum(float v) {
   return v;
 }
 
+#ifndef VIB3_DOWN_SCALAR_PAGES
+#define VIB3_DOWN_SCALAR_PAGES 1  // (build-time switch of the scalar page-address path)
+#endif
+constexpr int kDownScalarSlots = 16;  // most slots whose page addresses k_down_rows keeps in SGPRs
+
 template <int R, int J, int NB, bool ONE>  // ONE: the whole row in one pass (cpr <= CPP)
 __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
   VIB3_TRACE_POINT(0);
@@ -639,21 +656,41 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
   // then reads no page table (a scalar table read per batch would delay every batch's loads
   // by its latency)
   const bool group_pages = a.rpp % R == 0;
+  // With the gate/up kernel's list of page addresses, whole row groups per page and few slots,
+  // the page addresses come through scalar loads (one round trip, no ids), which leaves the
+  // vector memory counter to the activations: those go out first, and waiting for the
+  // addresses does not wait for them.
+  const bool scalar_pages =
+      VIB3_DOWN_SCALAR_PAGES && a.bases && group_pages && ns <= kDownScalarSlots;
+  const int r0 = min(R * g0, a.M - 1);
+  const int page0 = (int)(((uint64_t)(uint32_t)r0 * a.magic) >> 32);  // page of this wave's rows
   uint64_t my_t = 0, my_base = 0;
   float my_w = 1.0f;
   if (lane < ns) {
+    if (lane < top_k) my_w = a.wts[lane];
+    else if (a.shared_w) my_w = a.shared_w[lane - top_k];  // sigmoid gate of a shared expert
+  }
+  if (!scalar_pages && lane < ns) {
     const uint64_t* t =
         lane < top_k ? a.routed_table + ((size_t)a.ids[lane] * 3 + 2) * a.max_pages
                      : a.shared_table + ((size_t)(lane - top_k) * 3 + 2) * a.max_pages;
     my_t = (uint64_t)(uintptr_t)t;
-    if (lane < top_k) my_w = a.wts[lane];
-    else if (a.shared_w) my_w = a.shared_w[lane - top_k];  // sigmoid gate of a shared expert
     if (group_pages) {
       typedef __attribute__((address_space(1))) const uint64_t gtab;
-      const int r0 = min(R * g0, a.M - 1);
-      my_base = *(gtab*)(t + (int)(((uint64_t)(uint32_t)r0 * a.magic) >> 32));
+      my_base = *(gtab*)(t + page0);
     }
   }
+  auto scalar_bases = [&]() {  // page addresses from the list the gate/up kernel wrote
+    uint64_t bs[kDownScalarSlots];
+#pragma unroll
+    for (int s = 0; s < kDownScalarSlots; s++)  // slots past the last repeat it
+      bs[s] = ld_table(a.bases + (size_t)min(s, ns - 1) * a.bases_stride + page0);
+    __builtin_amdgcn_sched_barrier(0);  // (all loads issued before the first wait)
+    uint64_t base = 0;
+#pragma unroll
+    for (int s = 0; s < kDownScalarSlots; s++) base = lane == s ? bs[s] : base;
+    return base;
+  };
 
   // one row group per wave (the launcher sizes the grid so); its batches are (slot, pass),
   // passes innermost
@@ -676,8 +713,10 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
     const uint8_t* d = nullptr;
     const uint16_t* sc = nullptr;
     if (group_pages) {  // every lane its own row of the group's page
-      page_row((const uint8_t*)(uintptr_t)rl64(my_base, q.s), min(R * g0 + grp, a.M - 1),
-               a.rpp, a.M, a.magic, pk, ng, d, sc);
+      const uint64_t pb = rl64(my_base, q.s);
+      past = past || pb == 0;  // (no address: a down stage launched before any gate/up stage)
+      page_row((const uint8_t*)(uintptr_t)pb, min(R * g0 + grp, a.M - 1), a.rpp, a.M, a.magic,
+               pk, ng, d, sc);
     } else {
       const MatRef m{(const uint64_t*)(uintptr_t)rl64(my_t, q.s), nullptr, nullptr, a.rpp, a.M,
                      a.magic};
@@ -799,10 +838,23 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
     // (cached) activations, so waiting for the activations does not wait for the weights
     uint4 raw[3][4];
     load_raw((int)threadIdx.x, raw);
+    if (scalar_pages) {
+      __builtin_amdgcn_sched_barrier(0);  // (the activation loads issue first)
+      my_base = scalar_bases();
+    }
     // (also for a wave with no batches: every position is valid, and a branch here would make
     // the waits below count for both cases, i.e. wait for the weights too)
 #pragma unroll
     for (int b = 0; b + 1 < NB; b++) start(buf[b], pos[b], false);  // rows clamp to M - 1
+#ifdef VIB3_TRACE
+    VIB3_TRACE_POINT(7);  // first batches issued
+#pragma unroll
+    for (int u = 0; u < 3; u++)
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        asm volatile("" ::"v"(raw[u][q].x), "v"(raw[u][q].y), "v"(raw[u][q].z), "v"(raw[u][q].w));
+    VIB3_TRACE_POINT(6);  // activations arrived
+#endif
     stage((int)threadIdx.x, raw);
   }
   for (int i0 = (int)threadIdx.x + 3 * bd; i0 < nitem; i0 += 3 * bd) {
@@ -825,11 +877,16 @@ __global__ __launch_bounds__(512) void k_down_rows(DownArgs a) {
       pos[nb] = advance(pos[(nb + NB - 1) % NB]);
       // (the explicit wait: see k_int4_rows; here it keeps the compiler's count exact with
       // the past-the-end batches, which read the cached intermediate instead of weights)
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      // (batch b's loads done: at most the NB - 2 batches issued after it still loading)
+      VIB3_WAIT_VM((NB - 2) * 2 * J);
       start(buf[nb], pos[nb], k + b + NB - 1 >= n);
       finish(buf[b], pos[b], k + b < n);
+#ifdef VIB3_TRACE
+      if (k + b == 0) VIB3_TRACE_POINT(4);  // first batch reduced
+#endif
     }
   }
+  VIB3_TRACE_POINT(5);
   // stored after the loop: a store inside it would share the load counter with the weight
   // loads, and the compiler then waits for all of them at the loop head
   const int r = R * g0 + grp;
@@ -923,11 +980,17 @@ static void launch_rows_t(RowsArgs& a, hipStream_t s, KTime t) {
   if (!a.routed_table) return launch_rows_p<N, D, S, false>(a, s, t);
   return launch_rows_p<N, D, S, true>(a, s, t);
 }
+bool rows_write_bases(const RowsArgs& a) {  // k_int4_rows (one k pass, paged) writes them
+  int nch = 1, ks = 1;
+  return a.routed_table && a.M > 0 && a.nslots > 0 && !pick_nch(a.K / 32, 4, nch, ks) && ks == 1;
+}
+
 int launch_rows(RowsArgs a, bool dual, hipStream_t s, KTime t) {
   const int cpr = a.K / 32;
   int nch = 1, ks = 1;
   if (pick_nch(cpr, 4, nch, ks)) return VIB3_ERR_UNSUPPORTED;
   a.KS = ks;
+  if (!rows_write_bases(a)) a.down_bases = nullptr;
   if (a.RPT <= 0 || a.RPT > kWave) a.RPT = 8;
   if (a.M <= 0 || a.nslots <= 0) return 0;
   // f32 activations: int16 block fixed point where the caller asks for it (paged layer

@@ -90,6 +90,10 @@ struct RowsArgs {
   // f32 activations of a paged launch as int16 block fixed point (one integer dot product per
   // weight pair, error 2^-16 of each 32-chunk's largest value) instead of the hi + lo split
   int x_i16;
+  // paged launches that route: block 0 also writes the down segment's page addresses of every
+  // slot here ([nslots][down_pages], slot order), for the down kernel that follows (or null)
+  uint64_t* down_bases;
+  int down_pages;
 };
 
 // Down projection of every slot for a block of RB output rows plus the weighted expert sum.
@@ -101,6 +105,10 @@ struct DownArgs {
   const uint64_t* routed_table;
   const uint64_t* shared_table;
   const uint16_t* ids;
+  // page addresses of the down segment per slot ([nslots][bases_stride], written by the
+  // gate/up kernel of the same layer call), or null: the kernel reads the page tables itself
+  const uint64_t* bases;
+  int bases_stride;
   const float* wts;
   int top_k;
   int max_pages;
@@ -134,6 +142,8 @@ struct GenericArgs {
 };
 
 int launch_rows(RowsArgs a, bool dual, hipStream_t s, KTime t = {});
+// whether launch_rows(a) lists the down page addresses at a.down_bases (when given)
+bool rows_write_bases(const RowsArgs& a);
 int launch_down(DownArgs a, hipStream_t s, KTime t = {});
 int launch_generic(GenericArgs a, bool dual, hipStream_t s);
 // RMSNorm of x into xn (norm_w set) and the shared experts' sigmoid gates (gate_w set).
