@@ -192,3 +192,32 @@ def test_norm_needs_f32_stream():
                              norm_weight=_dev16(_f16(1024, 10, 0.1, 1.0)))
     with pytest.raises(Vib3Error):
         layer.launch(moe.make_activation(1024, 0, SEED))  # bf16 x with a norm: unsupported
+
+
+@pytest.mark.parametrize("hidden,inter,E,k,ns", [(1024, 256, 16, 4, 2), (7168, 2048, 384, 8, 1)])
+def test_fused_prologue_equals_prologue_kernel(hidden, inter, E, k, ns, monkeypatch):
+    """The gate/up kernel that normalises x and computes the shared gates itself gives the
+    layer of the separate prologue kernel bit for bit (same summation orders), over several
+    tokens, with and without the residual."""
+    from vib3_amd import moe
+    from vib3_amd._lib import DT_BF16, ROUTER_SIGMOID
+    _say(f"case: fused prologue hidden={hidden} E={E} k={k} shared={ns}")
+    sh = _shape(moe, DT_BF16, hidden, inter, E, ns)
+    bank = moe.Int4ExpertBank(sh, layer=5, seed=SEED)
+    w, bias = moe.make_router(sh, 5, SEED, 0.02, 0.1)
+    layer = moe.MoeInt4Layer(bank, w, bias, top_k=k, scoring_mode=ROUTER_SIGMOID,
+                             scaling_factor=2.827, normalize=True,
+                             norm_weight=_dev16(_f16(hidden, 10, 0.1, 1.0)), norm_eps=1e-6,
+                             shared_gate=_dev16(_f16(ns * hidden, 11, 0.02)))
+    for t in range(3):
+        x = torch.from_numpy(_f32(hidden, 20 + t, 20.0)).cuda()
+        res = torch.from_numpy(_f32(hidden, 30 + t, 20.0)).cuda() if t != 1 else None
+        monkeypatch.delenv("VIB3_PROLOGUE_KERNEL", raising=False)
+        fused = layer.launch(x, residual=res).cpu().numpy().copy()
+        ids_f = layer.ids.cpu().numpy().copy()
+        monkeypatch.setenv("VIB3_PROLOGUE_KERNEL", "1")
+        sep = layer.launch(x, residual=res).cpu().numpy().copy()
+        ids_s = layer.ids.cpu().numpy().copy()
+        monkeypatch.delenv("VIB3_PROLOGUE_KERNEL")
+        assert np.array_equal(ids_f, ids_s)
+        assert np.array_equal(fused.view(np.uint32), sep.view(np.uint32)), t

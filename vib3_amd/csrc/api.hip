@@ -391,11 +391,26 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only,
   hipStream_t st = S(stream);
   auto run = [&](int i) { return only < 0 || only == i; };
 
-  // the activation the router and experts read: x, or RMSNorm(x) written by the prologue,
-  // which also computes the shared experts' gates (stage 0 with the router)
-  const void* xa = L->norm_weight ? (const void*)(ws + w.xn) : L->x;
+  // The activation the router and experts read: x, or RMSNorm(x). The gate/up kernel
+  // normalises x itself and computes the shared experts' gates where it can (fused routing,
+  // f32 stream in int16 chunks, hidden <= 8192); else the prologue kernel writes RMSNorm(x)
+  // and the gates first (stage 0 with the router).
+  const int x_i16 = getenv("VIB3_F32_SPLIT") ? 0 : 1;  // f32 stream: int16 chunks (A/B: split)
+  bool fuse_prologue = false;
+  if (L->norm_weight && !getenv("VIB3_PROLOGUE_KERNEL")) {
+    RowsArgs p{};
+    p.x = L->x; p.x_dt = L->x_dtype; p.x_i16 = x_i16; p.K = L->hidden; p.M = L->inter;
+    p.nslots = nslots; p.routed_table = L->page_table; p.route = router_mode(L);
+    p.router.D = L->hidden; p.router.w = L->router_w; p.router.x = L->x;
+    p.router.E = L->num_experts;
+    p.norm_w = (const uint16_t*)L->norm_weight;
+    p.gate_w = (const uint16_t*)L->shared_gate;
+    p.ngate = L->shared_gate ? L->num_shared : 0;
+    fuse_prologue = rows_fuse_prologue(p);
+  }
+  const void* xa = L->norm_weight && !fuse_prologue ? (const void*)(ws + w.xn) : L->x;
   const float* shared_w = L->shared_gate ? (const float*)(ws + w.shared_w) : nullptr;
-  if (run(0) && (L->norm_weight || L->shared_gate)) {
+  if (run(0) && !fuse_prologue && (L->norm_weight || L->shared_gate)) {
     const int rc = launch_moe_prologue(L->x, L->x_dtype, (const uint16_t*)L->norm_weight,
                                        L->norm_eps, L->hidden, (float*)(ws + w.xn),
                                        (const uint16_t*)L->shared_gate, L->num_shared,
@@ -469,7 +484,14 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only,
   a.out = ws + w.h; a.out_dt = h_dt; a.out_stride = (size_t)L->inter;
   a.route = route;
   a.router = router;
-  a.x_i16 = getenv("VIB3_F32_SPLIT") ? 0 : 1;  // f32 stream: int16 chunks (A/B knob: split)
+  a.x_i16 = x_i16;
+  if (fuse_prologue) {
+    a.norm_w = (const uint16_t*)L->norm_weight;
+    a.eps = L->norm_eps;
+    a.gate_w = (const uint16_t*)L->shared_gate;
+    a.ngate = L->shared_gate ? L->num_shared : 0;
+    a.shared_w = (float*)(ws + w.shared_w);
+  }
   // the gate/up kernel lists the down page addresses for the down kernel (a down stage alone
   // reads the list its gate/up stage left, like h and the ids)
   const bool bases = w.down_pages > 0 && w.down_pages <= L->max_pages && rows_write_bases(a);

@@ -98,6 +98,11 @@ struct XChunk {
   float xs8;                   // 8 * 2^-24 * sum of the chunk's activations
 };
 
+struct XWords {  // an XChunk as its 17 words (xs8 last)
+  uint32_t w[17];
+};
+static_assert(sizeof(XWords) == sizeof(XChunk), "XChunk is 17 words");
+
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 
 __device__ __forceinline__ float chunk_dot(const uint4 w, const XChunk& x) {
@@ -153,8 +158,9 @@ __device__ __forceinline__ bool make_chunk(const float* xv, XChunk& hi, XChunk& 
 
 // Activation modes of the INT4 row kernels: f16 pairs (exact for f16 / bf16 activations),
 // f32 split into hi + lo f16 pairs (two dot products per pair), or f32 as int16 block fixed
-// point per 32-element chunk (one integer dot product per pair).
-enum { kXf16 = 0, kXsplit = 1, kXi16 = 2 };
+// point per 32-element chunk (one integer dot product per pair); kXi16n: kXi16 of RMSNorm(x),
+// the norm fused into the kernel (x the f32 residual stream).
+enum { kXf16 = 0, kXsplit = 1, kXi16 = 2, kXi16n = 3 };
 
 // Chunk of 32 f32 activations as int16 pairs x_i = rint(x * 2^sh), sh = 15 - E with E the
 // exponent of the chunk's largest |x| (|x_i| <= 32767), in the slots of hi (the pair layout

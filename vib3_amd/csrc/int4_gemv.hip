@@ -17,6 +17,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "norm.h"
 #include "router_dot.h"
 #include "select.h"
 
@@ -127,13 +128,26 @@ __device__ __forceinline__ void chunk_index(int ks, int g, int cpr, int (&cidx)[
 // Activation chunks of this lane (see chunk_index), converted to f16 pairs.
 template <int NCH, int XM>
 __device__ __forceinline__ void load_x(const void* x, int x_dt, int cpr, const int (&cidx)[NCH],
-                                       XChunk (&xh)[NCH], XChunk (&xl)[NCH]) {
+                                       XChunk (&xh)[NCH], XChunk (&xl)[NCH],
+                                       const uint16_t* nw = nullptr, float inv = 1.0f) {
 #pragma unroll
   for (int j = 0; j < NCH; j++) {
     if (cidx[j] < cpr) {
       float xv[32];
       load_chunk_act(x, x_dt, cidx[j], xv);
-      if (XM == kXi16) {
+      if (XM == kXi16n) {  // RMSNorm(x), element by element as the standalone norm writes it
+        const uint4* np = (const uint4*)(nw + 32 * (size_t)cidx[j]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const uint4 v = np[i];
+          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int k = 0; k < 8; k++)
+            xv[8 * i + k] = norm_mul(xv[8 * i + k], inv,
+                                     f16_to_f32((uint16_t)(w[k >> 1] >> (16 * (k & 1)))));
+        }
+      }
+      if (XM == kXi16 || XM == kXi16n) {
         make_chunk_i16(xv, xh[j], xl[j]);
       } else {
         make_chunk(xv, xh[j], xl[j]);
@@ -173,6 +187,10 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, size_t o, float v) 
 // stride over them (grid sized to the resident capacity), so all CUs stay busy to the end.
 // KS > 1: the KS waves of a team split one row's k range and combine through LDS.
 
+
+#ifndef VIB3_X_SHARED
+#define VIB3_X_SHARED 1  // (build-time switch: one wave converts the activations for all four)
+#endif
 
 template <int NCH, bool DUAL, int XM, bool PAGED>
 __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
@@ -257,7 +275,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   int kres = 0;
   auto finish = [&](const RowBatch<NCH, DUAL, 1>& buf) {
     float t0[1], t1[1];
-    reduce<NCH, DUAL, XM, 1>(buf, xh, xl, cidx, cpr, a.sdt, t0, t1);
+    reduce<NCH, DUAL, (XM == kXi16n ? kXi16 : XM), 1>(buf, xh, xl, cidx, cpr, a.sdt, t0, t1);
     const float v = rows_epilogue(DUAL, t0[0], t1[0]);
     if (lane == kres) res = v;
     kres++;
@@ -284,18 +302,40 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
       if (a.router.scores) a.router.scores[e] = v;
     }
   };
+  // Fused prologue (NORM): the residual stream in the norm's thread layout (x[t + 256 i]),
+  // issued first; the launcher guarantees fused routing with every router row in the split
+  // form below, and K <= 256 * kNormMax.
+  constexpr bool NORM = XM == kXi16n;
+  float xr[NORM ? kNormMax : 1];
+  if (NORM) {
+#pragma unroll
+    for (int i = 0; i < kNormMax; i++) {
+      const int d = (int)threadIdx.x + 256 * i;
+      xr[i] = ((const float*)a.x)[d < a.K ? d : 0];
+    }
+  }
   const bool split_row = fused && (int)blockIdx.x < E && router_seg_ok(a.router, 1, 4);
   RouterSegRaw<4> rrow;
-  if (split_row) router_seg_issue<4>(a.router, (int)blockIdx.x, 0, 1, rrow);
+  if (split_row) router_seg_issue<4, NORM>(a.router, (int)blockIdx.x, 0, 1, rrow, a.norm_w);
   VIB3_TRACE_POINT(11);  // router row issued
   // this launch's tag, read once the router row's loads are out
   if (fused && a.router.gen_word) a.router.gen = next_tag(*a.router.gen_word);
   const bool early_now = early && !(fused && (int)blockIdx.x < E);
   if (early_now) start(buf[0], 0, true, it0);
+  float inv = 1.0f;
+  if (NORM) {
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormMax; i++) {
+      const float v = (int)threadIdx.x + 256 * i < a.K ? xr[i] : 0.0f;
+      p = __builtin_fmaf(v, v, p);
+    }
+    inv = block_inv_rms(p, a.K, a.eps);
+  }
   if (fused) {
     int e = (int)blockIdx.x;
     if (split_row) {
-      publish(e, router_seg_finish<4>(a.router, 1, rrow));
+      publish(e, router_seg_finish<4, NORM>(a.router, 1, rrow, inv));
       VIB3_TRACE_POINT(12);  // router row published
       e += G;
     }
@@ -304,10 +344,67 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
       __syncthreads();  // router_row_dot's reduction buffer is reused by the next row
     }
   }
-  // the activations, while the routing is pending; the selecting wave of a launch without
-  // fused routing selects first (its loads would queue behind its early batch)
-  const bool sel_first = wave == 0 && !fused;
-  if (!sel_first) load_x<NCH, XM>(a.x, a.x_dt, cpr, cidx, xh, xl);
+  if (NORM && wave == 2 && (int)blockIdx.x < a.ngate) {
+    // Shared expert s = block's gate, by the block's third wave while the first selects and
+    // the second loads the activations:
+    // sigmoid(gate_w[s] . RMSNorm(x)) as the prologue kernel computes it (thread t of 256
+    // accumulates elements t + 256 i in i order, each wave's partials summed by wave_sum, the
+    // four wave sums pairwise); this one wave plays the four waves' threads in turn.
+    const uint16_t* gw = a.gate_w + (size_t)blockIdx.x * a.K;
+    float ws0 = 0.0f, ws1 = 0.0f, ws2 = 0.0f, ws3 = 0.0f;
+#pragma unroll 1
+    for (int vw = 0; vw < 4; vw++) {
+      const int t = vw * kWave + lane;
+      float acc = 0.0f;
+#pragma unroll
+      for (int h = 0; h < kNormMax; h += kNormMax / 2) {  // (half the loads at a time)
+        uint16_t gr[kNormMax / 2], nr[kNormMax / 2];
+        float xg[kNormMax / 2];
+#pragma unroll
+        for (int i = 0; i < kNormMax / 2; i++) {
+          const int d = min(t + 256 * (h + i), a.K - 1);
+          gr[i] = gw[d];
+          nr[i] = a.norm_w[d];
+          xg[i] = ((const float*)a.x)[d];
+        }
+#pragma unroll
+        for (int i = 0; i < kNormMax / 2; i++) {
+          const bool in = t + 256 * (h + i) < a.K;
+          const float xn = norm_mul(in ? xg[i] : 0.0f, inv, f16_to_f32(nr[i]));
+          acc = __builtin_fmaf(xn, in ? f16_to_f32(gr[i]) : 0.0f, acc);
+        }
+      }
+      const float v = wave_sum(acc);
+      ws0 = vw == 0 ? v : ws0;
+      ws1 = vw == 1 ? v : ws1;
+      ws2 = vw == 2 ? v : ws2;
+      ws3 = vw == 3 ? v : ws3;
+    }
+    if (lane == 0) {
+      const float g = (ws0 + ws1) + (ws2 + ws3);
+      a.shared_w[blockIdx.x] = 1.0f / (1.0f + expf(-g));
+    }
+  }
+  // The activation chunks, while the routing is pending. A lane's chunks depend on the lane
+  // only, so every wave of the workgroup holds the same ones: the second wave loads and
+  // converts them and the others copy them from LDS after the barrier below (a quarter of
+  // the cache traffic, and none of it ahead of the selecting wave's polls).
+  constexpr int XQ = XM == kXi16n ? kXi16 : XM;
+  constexpr int XLW = XQ == kXsplit ? 17 : XQ == kXi16 ? 1 : 0;  // words of xl kept
+  __shared__ uint32_t s_x[NCH * (17 + XLW) * kWave];
+  if (!VIB3_X_SHARED || wave == 1) {
+    load_x<NCH, XM>(a.x, a.x_dt, cpr, cidx, xh, xl, a.norm_w, inv);
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+      const auto hw = __builtin_bit_cast(XWords, xh[j]);
+      const auto lw = __builtin_bit_cast(XWords, xl[j]);
+#pragma unroll
+      for (int k = 0; k < 17; k++) s_x[(j * (17 + XLW) + k) * kWave + lane] = hw.w[k];
+#pragma unroll
+      for (int k = 0; k < XLW; k++)
+        s_x[(j * (17 + XLW) + 17 + k) * kWave + lane] = lw.w[XLW == 1 ? 16 : k];
+    }
+  }
   VIB3_TRACE_POINT(1);
   if (PAGED && top_k > 0 && wave == 0) {
     // the selection is on every routed row's critical path: issue ahead of the streaming
@@ -330,9 +427,21 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     __builtin_amdgcn_s_setprio(0);
     VIB3_TRACE_POINT(2);
   }
-  if (sel_first) load_x<NCH, XM>(a.x, a.x_dt, cpr, cidx, xh, xl);
   __syncthreads();
   VIB3_TRACE_POINT(3);
+  if (VIB3_X_SHARED && wave != 1) {
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+      XWords hw, lw{};
+#pragma unroll
+      for (int k = 0; k < 17; k++) hw.w[k] = s_x[(j * (17 + XLW) + k) * kWave + lane];
+#pragma unroll
+      for (int k = 0; k < XLW; k++)
+        lw.w[XLW == 1 ? 16 : k] = s_x[(j * (17 + XLW) + 17 + k) * kWave + lane];
+      xh[j] = __builtin_bit_cast(XChunk, hw);
+      xl[j] = __builtin_bit_cast(XChunk, lw);
+    }
+  }
   // block 0's first wave: the down segment's page addresses of every slot, for the down
   // kernel (one table round trip there less)
   if (PAGED && a.down_bases && blockIdx.x == 0 && wave == 0) {
@@ -953,19 +1062,25 @@ static int env_int(const char* name, int dflt) {
 }
 
 template <int N, bool D, int S, bool P>
+static int rows_grid(const RowsArgs& a) {  // workgroups of a k_int4_rows launch
+  auto k = k_int4_rows<N, D, S, P>;
+  const int items = a.nslots * a.M;
+  const int want = (items + 3) / 4;
+  int cap = resident_blocks(k, 256);
+  const int per_cu = env_int("VIB3_ROWS_BLOCKS_PER_CU", 0);
+  if (per_cu > 0 && per_cu * device_cus() < cap) cap = per_cu * device_cus();
+  const int floor_blocks = (items + 4 * kWave - 1) / (4 * kWave);  // <= 64 items per wave
+  if (cap < floor_blocks) cap = floor_blocks;
+  return want < cap ? want : cap;
+}
+
+template <int N, bool D, int S, bool P>
 static void launch_rows_p(RowsArgs& a, hipStream_t s, KTime t) {
-  if (a.KS == 1) {
-    auto k = k_int4_rows<N, D, S, P>;
-    const int items = a.nslots * a.M;
-    const int want = (items + 3) / 4;
-    int cap = resident_blocks(k, 256);
-    const int per_cu = env_int("VIB3_ROWS_BLOCKS_PER_CU", 0);
-    if (per_cu > 0 && per_cu * device_cus() < cap) cap = per_cu * device_cus();
-    const int floor_blocks = (items + 4 * kWave - 1) / (4 * kWave);  // <= 64 items per wave
-    if (cap < floor_blocks) cap = floor_blocks;
-    const int grid = want < cap ? want : cap;
-    hipExtLaunchKernelGGL(k, dim3((unsigned)grid), dim3(256), 0, s, t.start, t.stop, 0, a);
-  } else {
+  if (S == kXi16n || a.KS == 1) {
+    const int grid = rows_grid<N, D, S, P>(a);
+    hipExtLaunchKernelGGL((k_int4_rows<N, D, S, P>), dim3((unsigned)grid), dim3(256), 0, s,
+                          t.start, t.stop, 0, a);
+  } else if constexpr (S != kXi16n) {
     auto k = k_int4_rows_ksplit<N, D, S, P>;
     const int teams = 4 / a.KS;
     dim3 grid((unsigned)((a.M + teams * a.RPT - 1) / (teams * a.RPT)), (unsigned)a.nslots);
@@ -976,13 +1091,33 @@ static void launch_rows_p(RowsArgs& a, hipStream_t s, KTime t) {
 
 template <int N, bool D, int S>
 static void launch_rows_t(RowsArgs& a, hipStream_t s, KTime t) {
-  if (S == kXi16) return launch_rows_p<N, D, kXi16, true>(a, s, t);  // paged launches only
+  if (S == kXi16n) return launch_rows_p<N, D, kXi16n, true>(a, s, t);  // paged launches only
+  if (S == kXi16) return launch_rows_p<N, D, kXi16, true>(a, s, t);
   if (!a.routed_table) return launch_rows_p<N, D, S, false>(a, s, t);
   return launch_rows_p<N, D, S, true>(a, s, t);
 }
 bool rows_write_bases(const RowsArgs& a) {  // k_int4_rows (one k pass, paged) writes them
   int nch = 1, ks = 1;
   return a.routed_table && a.M > 0 && a.nslots > 0 && !pick_nch(a.K / 32, 4, nch, ks) && ks == 1;
+}
+
+// The fused prologue needs the int16 mode of a paged one-pass launch with fused routing, every
+// router row in the kernel's split form on a workgroup of its own, and K <= 256 * kNormMax.
+bool rows_fuse_prologue(const RowsArgs& a) {
+  int nch = 1, ks = 1;
+  if (!a.norm_w || a.x_dt != VIB3_DT_F32 || !a.x_i16 || !rows_write_bases(a) ||
+      a.route != kRouteFused || a.K > 256 * kNormMax || (a.ngate > 0 && !a.gate_w) ||
+      a.ngate > a.router.E)
+    return false;
+  const RouterArgs& r = a.router;
+  if (r.D != a.K || r.D % 8 || r.D / 8 > 4 * 256 || ((uintptr_t)r.w & 15) || ((uintptr_t)a.x & 15) ||
+      ((uintptr_t)a.norm_w & 15) || r.x != a.x)
+    return false;
+  pick_nch(a.K / 32, 4, nch, ks);
+  const int grid = nch == 1   ? rows_grid<1, true, kXi16n, true>(a)
+                   : nch == 2 ? rows_grid<2, true, kXi16n, true>(a)
+                              : rows_grid<4, true, kXi16n, true>(a);
+  return r.E <= grid;
 }
 
 int launch_rows(RowsArgs a, bool dual, hipStream_t s, KTime t) {
@@ -995,11 +1130,16 @@ int launch_rows(RowsArgs a, bool dual, hipStream_t s, KTime t) {
   if (a.M <= 0 || a.nslots <= 0) return 0;
   // f32 activations: int16 block fixed point where the caller asks for it (paged layer
   // launches with k in one pass), else the hi + lo f16 split
-  const int xm = a.x_dt != VIB3_DT_F32 ? kXf16
-                 : (a.x_i16 && a.routed_table && ks == 1) ? kXi16 : kXsplit;
+  int xm = a.x_dt != VIB3_DT_F32 ? kXf16
+           : (a.x_i16 && a.routed_table && ks == 1) ? kXi16 : kXsplit;
+  if (a.norm_w) {  // a fused prologue asked for: the only mode that applies the norm
+    if (!dual || !rows_fuse_prologue(a)) return VIB3_ERR_UNSUPPORTED;
+    xm = kXi16n;
+  }
 #define VIB3_ROWS(N, D)                                   \
   do {                                                    \
-    if (xm == kXi16) launch_rows_t<N, D, kXi16>(a, s, t); \
+    if (D && xm == kXi16n) launch_rows_t<N, true, kXi16n>(a, s, t); \
+    else if (xm == kXi16) launch_rows_t<N, D, kXi16>(a, s, t); \
     else if (xm == kXsplit) launch_rows_t<N, D, kXsplit>(a, s, t); \
     else launch_rows_t<N, D, kXf16>(a, s, t);             \
   } while (0)

@@ -94,6 +94,14 @@ struct RowsArgs {
   // slot here ([nslots][down_pages], slot order), for the down kernel that follows (or null)
   uint64_t* down_bases;
   int down_pages;
+  // fused sublayer prologue (fused routing, f32 x): x and router.x are the residual stream,
+  // which the kernel normalises (RMSNorm, weights norm_w); the second wave of workgroup s
+  // also stores shared expert s's sigmoid gate (gate_w row s . RMSNorm(x)) in shared_w[s]
+  const uint16_t* norm_w;
+  float eps;
+  const uint16_t* gate_w;
+  int ngate;
+  float* shared_w;
 };
 
 // Down projection of every slot for a block of RB output rows plus the weighted expert sum.
@@ -144,6 +152,8 @@ struct GenericArgs {
 int launch_rows(RowsArgs a, bool dual, hipStream_t s, KTime t = {});
 // whether launch_rows(a) lists the down page addresses at a.down_bases (when given)
 bool rows_write_bases(const RowsArgs& a);
+// whether launch_rows(a) fuses the RMSNorm / shared-gate prologue given in a.norm_w ...
+bool rows_fuse_prologue(const RowsArgs& a);
 int launch_down(DownArgs a, hipStream_t s, KTime t = {});
 int launch_generic(GenericArgs a, bool dual, hipStream_t s);
 // RMSNorm of x into xn (norm_w set) and the shared experts' sigmoid gates (gate_w set).

@@ -1,0 +1,38 @@
+// norm.h — pieces of the pre-MoE RMSNorm (vib3_rms_norm_f32, kernels.cu:921-955) shared by
+// the standalone prologue kernel and the gate/up kernel that fuses it.
+//
+// Thread t of a 256-thread workgroup accumulates x[d]^2 for d = t, t + 256, ... with fused
+// multiply-adds, the 256 partials are summed by a halving tree, then rms = sqrt(ss / D + eps)
+// and inv = 1 / rms (both correctly rounded); y[d] = (x[d] * inv) * w[d] with two rounded
+// products. Every workgroup that follows this order computes the same inverse RMS, bit for bit.
+#pragma once
+
+#include "common.h"
+
+namespace vib3 {
+
+constexpr int kNormMax = 32;  // elements per thread: D <= 256 * kNormMax
+
+// Inverse RMS from each thread's partial sum (the halving tree over the workgroup's 256
+// threads; every thread gets the result).
+__device__ inline float block_inv_rms(float p, int D, float eps) {
+  __shared__ float ss[256];
+  const int tid = (int)threadIdx.x;
+  ss[tid] = p;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) ss[tid] += ss[tid + s];
+    __syncthreads();
+  }
+  const float rms = sqrtf(ss[0] / (float)D + eps);
+  const float inv = 1.0f / rms;
+  __syncthreads();  // ss is reused by the next call
+  return inv;
+}
+
+__device__ __forceinline__ float norm_mul(float x, float inv, float w) {
+#pragma clang fp contract(off)
+  return x * inv * w;
+}
+
+}  // namespace vib3

@@ -12,13 +12,13 @@
 // and still produce the single-workgroup reference result bit for bit.
 #include "common.h"
 #include "kernels.h"
+#include "norm.h"
 
 namespace vib3 {
 
 // Inverse RMS of x[0..D) for a 256-thread workgroup, in the reference's summation order.
 // Up to 8192 elements every load is issued before the first add (one round trip).
 __device__ float wg_inv_rms(const float* x, int D, float eps) {
-  __shared__ float ss[256];
   const int tid = (int)threadIdx.x;
   float p = 0.0f;
   if (D <= 256 * 32) {
@@ -33,21 +33,7 @@ __device__ float wg_inv_rms(const float* x, int D, float eps) {
       p = __builtin_fmaf(v, v, p);
     }
   }
-  ss[tid] = p;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (tid < s) ss[tid] += ss[tid + s];
-    __syncthreads();
-  }
-  const float rms = sqrtf(ss[0] / (float)D + eps);
-  const float inv = 1.0f / rms;
-  __syncthreads();  // ss is reused by the caller's next call
-  return inv;
-}
-
-__device__ __forceinline__ float norm_mul(float x, float inv, float w) {
-#pragma clang fp contract(off)
-  return x * inv * w;
+  return block_inv_rms(p, D, eps);
 }
 
 __device__ __forceinline__ float norm_elem(float x, float inv, uint16_t w) {
@@ -92,7 +78,7 @@ __global__ void k_sigmoid_gated_acc(float* out, const uint16_t* e, const float* 
 // Thread t holds elements t + 256 i (i < kProMax, D <= 256 * kProMax): the layout of the
 // reference's partial sums, so every load of a workgroup is issued at once (one round trip)
 // and the normalised values it writes are already in its registers.
-constexpr int kProMax = 32;
+constexpr int kProMax = kNormMax;
 
 struct PrologueArgs {
   const void* x;
@@ -138,18 +124,10 @@ __global__ __launch_bounds__(256) void k_moe_prologue(PrologueArgs a) {
   }
   float inv = 1.0f;
   if (a.norm_w) {
-    __shared__ float ss[256];
     float p = 0.0f;
 #pragma unroll
     for (int i = 0; i < kProMax; i++) p = __builtin_fmaf(xv[i], xv[i], p);  // zeros past D
-    ss[tid] = p;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-      if (tid < s) ss[tid] += ss[tid + s];
-      __syncthreads();
-    }
-    const float rms = sqrtf(ss[0] / (float)D + a.eps);
-    inv = 1.0f / rms;
+    inv = block_inv_rms(p, D, a.eps);
 #pragma unroll
     for (int i = 0; i < kProMax; i++) xv[i] = norm_mul(xv[i], inv, wv[i]);
   }

@@ -4,6 +4,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "norm.h"
 
 namespace vib3 {
 
@@ -96,6 +97,7 @@ __device__ inline float router_row_dot(const RouterArgs& a, int e) {
 template <int U>
 struct RouterSegRaw {
   uint4 w[U][2], x[U][2];
+  uint4 n[U];  // RMSNorm weights (f16) of the groups, when the norm is fused
 };
 
 __device__ inline bool router_seg_ok(const RouterArgs& a, int parts, int U) {
@@ -103,9 +105,11 @@ __device__ inline bool router_seg_ok(const RouterArgs& a, int parts, int U) {
          (((uintptr_t)a.x) & 15) == 0;
 }
 
-template <int U>
+// NORM: x is the f32 residual stream and the dot product takes RMSNorm(x) (weights nw, the
+// inverse RMS given to finish()), element by element as the standalone norm writes it.
+template <int U, bool NORM = false>
 __device__ inline void router_seg_issue(const RouterArgs& a, int e, int part, int parts,
-                                        RouterSegRaw<U>& r) {
+                                        RouterSegRaw<U>& r, const uint16_t* nw = nullptr) {
   const int tid = (int)threadIdx.x, n8 = a.D / (8 * parts);
   const int wsz = a.w_dt == VIB3_DT_F32 ? 32 : 16, xsz = a.x_dt == VIB3_DT_F32 ? 32 : 16;
   const size_t g0 = (size_t)part * n8;  // first 8-element group of the segment
@@ -119,6 +123,7 @@ __device__ inline void router_seg_issue(const RouterArgs& a, int e, int part, in
     r.w[u][1] = ld_stream(row + (size_t)ic * wsz + (wsz - 16));
     r.x[u][0] = *(const uint4*)(xs + (size_t)ic * xsz);
     r.x[u][1] = *(const uint4*)(xs + (size_t)ic * xsz + (xsz - 16));
+    if (NORM) r.n[u] = *(const uint4*)(nw + (g0 + (size_t)ic) * 8);
   }
 }
 
@@ -138,8 +143,9 @@ __device__ inline void raw8(const uint4 (&v)[2], int dt, float* o) {
   }
 }
 
-template <int U>
-__device__ inline float router_seg_finish(const RouterArgs& a, int parts, const RouterSegRaw<U>& r) {
+template <int U, bool NORM = false>
+__device__ inline float router_seg_finish(const RouterArgs& a, int parts, const RouterSegRaw<U>& r,
+                                          float inv = 1.0f) {
   __shared__ float red[4];
   const int tid = (int)threadIdx.x, n8 = a.D / (8 * parts);
   float acc = 0.0f;
@@ -149,6 +155,12 @@ __device__ inline float router_seg_finish(const RouterArgs& a, int parts, const 
       float w[8], x[8];
       raw8(r.w[u], a.w_dt, w);
       raw8(r.x[u], a.x_dt, x);
+      if (NORM) {
+        const uint32_t nv[4] = {r.n[u].x, r.n[u].y, r.n[u].z, r.n[u].w};
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+          x[j] = norm_mul(x[j], inv, f16_to_f32((uint16_t)(nv[j >> 1] >> (16 * (j & 1)))));
+      }
 #pragma unroll
       for (int j = 0; j < 8; j++) acc = __builtin_fmaf(x[j], w[j], acc);
     }
