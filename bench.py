@@ -326,6 +326,11 @@ def bench_fp4(args, cfg) -> int:
     nbytes = K * ebytes + H * 4 + H // 2 + H // 32 + 2 * H * 4
     gbs = nbytes / (us * 1e-6) / 1e9
     log(f"[bench] fp4 fused: {us:.2f} us/layer, {gbs:.0f} GB/s")
+    traffic = None  # HBM bytes per step of the three launches, from the committed PMC summary
+    tpath = os.path.join(ROOT, "profiles", "traffic_fp4.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = sum(v["hbm_bytes"] for v in json.load(f)["kernels"].values())
     out_line = {
         "metric": "fused NVFP4 MoE layer decode us (batch 1, Kimi-K2.5 shape)",
         "value": round(us, 3), "unit": "us/layer", "n_gpus": 1, "steps": args.steps,
@@ -337,7 +342,8 @@ def bench_fp4(args, cfg) -> int:
                    "algorithmic_bytes_per_layer": nbytes},
         "roofline": {"bound": "hbm", "kernel": "k_fp4_quant_act + k_fp4_gateup + k_fp4_down (whole step)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": "profiles/traffic_fp4.json" if traffic else None},
         "cpu_baseline": None,
     }
     print(json.dumps(out_line), flush=True)

@@ -55,7 +55,7 @@ def pmc(db: str) -> None:
 
 def _kernel_key(name: str) -> str:
     """`void vib3::k_mx_gemm<true, 4>(vib3::MxArgs)` -> `k_mx_gemm<true, 4>`."""
-    short = name.split("vib3::", 1)[-1]
+    short = name.replace("(anonymous namespace)::", "").split("vib3::", 1)[-1]
     depth = 0
     for i, ch in enumerate(short):
         depth += ch == "<"
