@@ -485,6 +485,7 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only,
   a.route = route;
   a.router = router;
   a.x_i16 = x_i16;
+  a.pre_shared = getenv("VIB3_PRE_SHARED") ? atoi(getenv("VIB3_PRE_SHARED")) : 1;  // (A/B knob)
   if (fuse_prologue) {
     a.norm_w = (const uint16_t*)L->norm_weight;
     a.eps = L->norm_eps;

@@ -207,6 +207,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // per slot: page-table row of each matrix (resolved once; a 16-bit id load in the loop
   // would be a vector load whose wait drains all prefetched weight loads)
   __shared__ const uint64_t* s_tab[16][2];
+  __shared__ int s_xready;  // the second wave's activation copy is in LDS (pre-streaming)
   chunk_index<NCH>(0, a.g, cpr, cidx, gidx);
   const int items = a.nslots * a.M;
   const int stride = (int)gridDim.x * 4;
@@ -220,6 +221,17 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     const int v = q + top_k;
     return v >= nslots ? v - nslots : v;
   };
+  // A wave's items. Normally item k is it0 + k * stride. With a.pre_shared (fused routing with
+  // shared experts; set by the launcher), the shared-expert items [0, S) go to waves 1-3 of
+  // every workgroup, which stream them while wave 0 waits for the routing (after their
+  // workgroup's router row), and every wave takes the routed items S + it0 + k * stride after
+  // them: the stream that waits for the selection is one item shorter.
+  const int NP = (int)gridDim.x * 3, S = (nslots - top_k) * M;
+  const bool pre = a.pre_shared && wave >= 1;
+  const int u = (int)blockIdx.x * 3 + wave - 1;
+  const int cs = pre ? max(0, (S - u + NP - 1) / max(NP, 1)) : 0;  // this wave's shared items
+  const int rbase = a.pre_shared ? S + it0 : it0;
+  auto item_at = [&](int k) { return k < cs ? u + k * NP : rbase + (k - cs) * stride; };
   auto shared_table_of = [&](int slot, int which) {
     return a.shared_table + ((size_t)(slot - top_k) * 3 + which) * a.max_pages;
   };
@@ -232,8 +244,9 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // start() is issued unconditionally, also for a batch past the last item (its loads then
   // read the activation vector). A branch around the loads would leave the compiler unsure
   // how many loads are in flight.
-  auto start = [&](RowBatch<NCH, DUAL, 1>& buf, int k, bool direct, int item) {
-    const bool past = item >= items;
+  auto start = [&](RowBatch<NCH, DUAL, 1>& buf, int k, bool direct, int item,
+                   bool dummy = false) {
+    const bool past = dummy || item >= items;
     MatRef m0, m1;
     int row;
     if (PAGED) {
@@ -280,13 +293,13 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     if (lane == kres) res = v;
     kres++;
   };
-  const bool have = it0 < items;
+  const bool have = item_at(0) < items;
   if (PAGED && wave == 0 && lane < nslots && lane >= top_k) {
     s_tab[lane][0] = shared_table_of(lane, 0);
     s_tab[lane][1] = shared_table_of(lane, 1);
   }
   // a shared-expert row needs no routing: start its loads before the selection
-  const bool early = have && PAGED && slot_of(it0 / M) >= top_k;
+  const bool early = have && PAGED && !a.pre_shared && slot_of(it0 / M) >= top_k;
   // Fused routing: workgroup b computes router rows b, b + grid, ... and publishes each as a
   // tagged slot. The first row's loads go out before anything else, and a workgroup computing
   // a router row starts its expert stream only after the selection, so the CU's memory
@@ -318,6 +331,10 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   RouterSegRaw<4> rrow;
   if (split_row) router_seg_issue<4, NORM>(a.router, (int)blockIdx.x, 0, 1, rrow, a.norm_w);
   VIB3_TRACE_POINT(11);  // router row issued
+  if (a.pre_shared) {  // (LDS holds whatever the CU's last workgroup left)
+    if (threadIdx.x == 0) s_xready = 0;
+    __syncthreads();
+  }
   // this launch's tag, read once the router row's loads are out
   if (fused && a.router.gen_word) a.router.gen = next_tag(*a.router.gen_word);
   const bool early_now = early && !(fused && (int)blockIdx.x < E);
@@ -392,6 +409,19 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   constexpr int XQ = XM == kXi16n ? kXi16 : XM;
   constexpr int XLW = XQ == kXsplit ? 17 : XQ == kXi16 ? 1 : 0;  // words of xl kept
   __shared__ uint32_t s_x[NCH * (17 + XLW) * kWave];
+  auto copy_x = [&]() {  // this wave's chunks from the second wave's LDS copy
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+      XWords hw, lw{};
+#pragma unroll
+      for (int k = 0; k < 17; k++) hw.w[k] = s_x[(j * (17 + XLW) + k) * kWave + lane];
+#pragma unroll
+      for (int k = 0; k < XLW; k++)
+        lw.w[XLW == 1 ? 16 : k] = s_x[(j * (17 + XLW) + 17 + k) * kWave + lane];
+      xh[j] = __builtin_bit_cast(XChunk, hw);
+      xl[j] = __builtin_bit_cast(XChunk, lw);
+    }
+  };
   if (!VIB3_X_SHARED || wave == 1) {
     load_x<NCH, XM>(a.x, a.x_dt, cpr, cidx, xh, xl, a.norm_w, inv);
 #pragma unroll
@@ -403,6 +433,11 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
 #pragma unroll
       for (int k = 0; k < XLW; k++)
         s_x[(j * (17 + XLW) + 17 + k) * kWave + lane] = lw.w[XLW == 1 ? 16 : k];
+    }
+    // waves that stream shared items before the barrier take the copy once this flag is set
+    if (VIB3_X_SHARED && a.pre_shared) {
+      wait_lgkm();
+      if (lane == 0) __hip_atomic_store(&s_xready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
   VIB3_TRACE_POINT(1);
@@ -427,21 +462,35 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     __builtin_amdgcn_s_setprio(0);
     VIB3_TRACE_POINT(2);
   }
+  if (pre && cs > 0) {
+    if (VIB3_X_SHARED && wave != 1) {  // (the second wave sets the flag without waiting)
+      while (__hip_atomic_load(&s_xready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+        __builtin_amdgcn_s_sleep(1);
+      copy_x();
+    }
+    // the shared items, straight from the kernel arguments, while the routing is pending;
+    // the same two-buffer pipeline as the loop below, the step after the last one a dummy
+    start(buf[0], 0, true, item_at(0));
+    for (int k = 0;; k += 2) {
+      bool done = false;
+#pragma unroll
+      for (int b = 0; b < 2; b++) {
+        const int ahead = k + b + 1;
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        start(buf[(b + 1) % 2], ahead, true, item_at(min(ahead, cs - 1)), ahead >= cs);
+        finish(buf[b]);
+        if (ahead >= cs) {
+          done = true;
+          break;
+        }
+      }
+      if (done) break;
+    }
+    VIB3_TRACE_POINT(13);  // shared items done
+  }
   __syncthreads();
   VIB3_TRACE_POINT(3);
-  if (VIB3_X_SHARED && wave != 1) {
-#pragma unroll
-    for (int j = 0; j < NCH; j++) {
-      XWords hw, lw{};
-#pragma unroll
-      for (int k = 0; k < 17; k++) hw.w[k] = s_x[(j * (17 + XLW) + k) * kWave + lane];
-#pragma unroll
-      for (int k = 0; k < XLW; k++)
-        lw.w[XLW == 1 ? 16 : k] = s_x[(j * (17 + XLW) + 17 + k) * kWave + lane];
-      xh[j] = __builtin_bit_cast(XChunk, hw);
-      xl[j] = __builtin_bit_cast(XChunk, lw);
-    }
-  }
+  if (VIB3_X_SHARED && wave != 1 && !(pre && cs > 0)) copy_x();
   // block 0's first wave: the down segment's page addresses of every slot, for the down
   // kernel (one table round trip there less)
   if (PAGED && a.down_bases && blockIdx.x == 0 && wave == 0) {
@@ -455,9 +504,16 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     }
   }
   if (!have) return;
+  if (item_at(cs) >= items) {  // shared items only: store them
+    if (lane < kres) {
+      const int item = item_at(lane), q = item / M;
+      store_out(a, (size_t)slot_of(q) * a.out_stride + (item - q * M), res);
+    }
+    return;
+  }
   if (PAGED) {
     // lane k <- this wave's k-th item (lanes past the end keep a valid page-table row)
-    const int item = min(it0 + lane * stride, items - 1);
+    const int item = min(item_at(lane), items - 1);
     {
       const int q = item / M;
       my_row = item - q * M;
@@ -466,22 +522,22 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
       my_t1 = (uint64_t)(uintptr_t)s_tab[slot][1];
     }
   }
-  if (!early_now) start(buf[0], 0, false, it0);
+  if (!early_now) start(buf[0], cs, false, item_at(cs));
   // Two buffers: item k + 1's loads go out, then item k is reduced. Each step first takes
   // delivery of everything in flight, so a wave has one item's loads (8 KB for a gate/up row
   // pair of k = 7168) outstanding at a time: streaming measured fastest with about that much
   // in flight per wave (two items per wave in flight, or a third buffer, measured slower).
   // The explicit wait also makes the step independent of how the compiler counts loads at
   // the loop head.
-  for (int k = 0;; k += 2) {
+  for (int k = cs;; k += 2) {
     bool done = false;
 #pragma unroll
     for (int b = 0; b < 2; b++) {
       const int ahead = k + b + 1;
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      start(buf[(b + 1) % 2], ahead, false, it0 + ahead * stride);
+      start(buf[(b + 1) % 2], ahead, false, item_at(ahead));
       finish(buf[b]);
-      if (it0 + (k + b + 1) * stride >= items) {
+      if (item_at(ahead) >= items) {
         done = true;
         break;
       }
@@ -489,7 +545,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     if (done) break;
   }
   if (lane < kres) {
-    const int item = it0 + lane * stride;
+    const int item = item_at(lane);
     const int q = item / M;
     store_out(a, (size_t)slot_of(q) * a.out_stride + (item - q * M), res);
   }
@@ -1078,9 +1134,19 @@ template <int N, bool D, int S, bool P>
 static void launch_rows_p(RowsArgs& a, hipStream_t s, KTime t) {
   if (S == kXi16n || a.KS == 1) {
     const int grid = rows_grid<N, D, S, P>(a);
+    if (a.pre_shared) {  // shared items before the selection: only where every wave keeps
+      // its items within the 64 lanes that hold them, and for f16 / bf16 activations (with
+      // the f32 stream the streaming waves slow the selecting wave more than they gain:
+      // sublayer 57.4-57.6 -> 57.7-57.9 us, against 53.7-54.0 -> 52.3-53.2 us for c2)
+      const int NP = grid * 3;
+      const int Sh = (a.nslots - a.top_k) * a.M, R = a.top_k * a.M, W = 4 * grid;
+      a.pre_shared = P && S == kXf16 && a.route == kRouteFused && Sh > 0 && NP > 0 &&
+                     (Sh + NP - 1) / NP + (R + W - 1) / W <= kWave;
+    }
     hipExtLaunchKernelGGL((k_int4_rows<N, D, S, P>), dim3((unsigned)grid), dim3(256), 0, s,
                           t.start, t.stop, 0, a);
   } else if constexpr (S != kXi16n) {
+    a.pre_shared = 0;
     auto k = k_int4_rows_ksplit<N, D, S, P>;
     const int teams = 4 / a.KS;
     dim3 grid((unsigned)((a.M + teams * a.RPT - 1) / (teams * a.RPT)), (unsigned)a.nslots);

@@ -94,6 +94,9 @@ struct RowsArgs {
   // slot here ([nslots][down_pages], slot order), for the down kernel that follows (or null)
   uint64_t* down_bases;
   int down_pages;
+  // fused routing with shared experts: stream the shared items on the workgroups without a
+  // router row while the routing is pending (the launcher clears it where it does not apply)
+  int pre_shared;
   // fused sublayer prologue (fused routing, f32 x): x and router.x are the residual stream,
   // which the kernel normalises (RMSNorm, weights norm_w); the second wave of workgroup s
   // also stores shared expert s's sigmoid gate (gate_w row s . RMSNorm(x)) in shared_w[s]
