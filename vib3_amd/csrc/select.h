@@ -295,27 +295,56 @@ __device__ inline void select_topk_regs(const RouterArgs& a, const float* scores
 // RouterArgs::spin_limit polls (kRouterSpinLimit normally) the wave records an error, which
 // the host reads with vib3_moe_int4_layer_status, and selects from what it has.
 
+#ifndef VIB3_POLL_GAP
+#define VIB3_POLL_GAP 20  // s_sleep units (64 clocks) between the two poll rounds in flight
+#endif
+constexpr int kPollGap = VIB3_POLL_GAP;
+
 template <int R>
 __device__ inline void select_topk_published(const RouterArgs& a, int* sel, float* selv,
                                              bool publish) {
   const int lane = lane_id();
   float sc[R], bs[R];
   load_bias<R>(a, bs);  // before the wait, off the critical path
-  for (int it = 0;; it++) {
+  // Two poll rounds in flight, the second issued about half a round trip after the first,
+  // so the last logit is seen about a quarter of a round trip sooner on average.
+  uint64_t va[R], vb[R];
+  const uint32_t want = a.gen ^ a.poll_xor;
+  auto issue = [&](uint64_t (&v)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; r++)
+      v[r] = __hip_atomic_load(a.slots + min(lane + r * kWave, a.E - 1), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+  };
+  auto ready = [&](const uint64_t (&v)[R]) {
     bool ok = true;
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-      const int e = min(lane + r * kWave, a.E - 1);
-      const uint64_t v = __hip_atomic_load(a.slots + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ok &= (uint32_t)(v >> 32) == (a.gen ^ a.poll_xor);
-      sc[r] = __uint_as_float((uint32_t)v);
-    }
-    if (__all(ok)) break;
-    if (it >= a.spin_limit) {
-      if (lane == 0) a.error[0] = 1;
+    for (int r = 0; r < R; r++) ok &= (uint32_t)(v[r] >> 32) == want;
+    return __all(ok);
+  };
+  auto take = [&](const uint64_t (&v)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; r++) sc[r] = __uint_as_float((uint32_t)v[r]);
+  };
+  issue(va);
+  __builtin_amdgcn_s_sleep(kPollGap);
+  issue(vb);
+  for (int it = 0;; it += 2) {
+    if (ready(va)) {
+      take(va);
       break;
     }
-    __builtin_amdgcn_s_sleep(1);
+    if (it >= a.spin_limit) {
+      if (lane == 0) a.error[0] = 1;
+      take(va);
+      break;
+    }
+    issue(va);
+    if (ready(vb)) {
+      take(vb);
+      break;
+    }
+    issue(vb);
   }
   select_topk_vals<R>(a, sc, bs, sel, selv, publish);
 }
