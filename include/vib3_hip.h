@@ -275,6 +275,16 @@ int vib3_launch_moe_int4_layer_stage(const vib3_moe_int4_layer *layer, int stage
  * (16-byte aligned) and act_scales[K/32] E8M0 = round(log2 amax) - 2 + 127 per 32 values. */
 int vib3_launch_quantize_activation_fp4(const void *input, void *act_fp4, void *act_scales,
                                         int K, void *stream);
+/* cuda_ffi.rs:781 (kernels.cu:6585-6727, kernels.rs:1641): RMSNorm of the f32 hidden state
+ * with f16 weights, quantized as vib3_launch_quantize_activation_fp4, in one launch;
+ * opt_f16_out (or NULL) receives the normalised values as f16. The sum of squares follows the
+ * reference's order; the inverse RMS is the correctly rounded 1/sqrtf where the reference
+ * uses the approximate rsqrtf. K a multiple of 32 (VIB3_ERR_UNSUPPORTED otherwise; the
+ * reference covers K/64 whole tiles). */
+int vib3_launch_fused_rms_norm_quantize_fp4(const void *input, const void *norm_weight,
+                                            void *act_fp4, void *act_scales, void *opt_f16_out,
+                                            int K, float eps, void *stream);
+
 /* cuda_ffi.rs:770 (kernels.cu:5252): the same. */
 int vib3_launch_quantize_activation_fp4_fast(const void *input, void *act_fp4,
                                              void *act_scales, int K, void *stream);

@@ -750,6 +750,50 @@ void v3o_fp4_quantize_act(const float *x, size_t k, uint8_t *codes, uint8_t *sca
     }
 }
 
+/* kernels.cu:6585-6702 vib3_fused_rms_norm_quantize_fp4_kernel (one 256-thread block):
+ * thread t accumulates x[d]^2 for d = t, t + 256, ... (a fused multiply-add each, as the CUDA
+ * compiler contracts `partial_ss += val * val`), each 32-thread warp sums its partials by the
+ * butterfly xor 16, 8, 4, 2, 1, thread 0 adds the eight warp sums in order from 0; then
+ * y[d] = (x[d] * inv) * f32(w[d]) (two rounded products), optionally rounded to f16, and y is
+ * quantized as v3o_fp4_quantize_act. The reference takes inv = rsqrtf(ss / K + eps), CUDA's
+ * approximate reciprocal square root; this restatement (and the GPU kernel) uses the
+ * correctly rounded 1 / sqrtf(ss / K + eps). */
+float v3o_fp4_norm_inv(const float *x, size_t k, float eps)
+{
+    float part[256];
+    for (size_t t = 0; t < 256; t++) {
+        float p = 0.0f;
+        for (size_t d = t; d < k; d += 256) p = fmaf(x[d], x[d], p);
+        part[t] = p;
+    }
+    float ws[8];
+    for (int w = 0; w < 8; w++) {
+        float v[32], nv[32];
+        for (int l = 0; l < 32; l++) v[l] = part[w * 32 + l];
+        for (int m = 16; m > 0; m >>= 1) {
+            for (int l = 0; l < 32; l++) nv[l] = v[l] + v[l ^ m];
+            for (int l = 0; l < 32; l++) v[l] = nv[l];
+        }
+        ws[w] = v[0];
+    }
+    float total = 0.0f;
+    for (int w = 0; w < 8; w++) total += ws[w];
+    return 1.0f / sqrtf(total / (float)k + eps);
+}
+
+void v3o_fused_rms_norm_quantize_fp4(const float *x, const uint16_t *w_f16, size_t k, float eps,
+                                     uint8_t *codes, uint8_t *scales, uint16_t *f16_out)
+{
+    float inv = v3o_fp4_norm_inv(x, k, eps);
+    float *y = (float *)malloc(k * sizeof(float));
+    for (size_t d = 0; d < k; d++) {
+        y[d] = x[d] * inv * v3o_f16_to_f32(w_f16[d]);
+        if (f16_out) f16_out[d] = v3o_f32_to_f16(y[d]);
+    }
+    v3o_fp4_quantize_act(y, k, codes, scales);
+    free(y);
+}
+
 /* Code of element k of a split-half vector (byte k/32*16 + k%16, high nibble for k%32 >= 16). */
 static uint8_t split_code(const uint8_t *codes, size_t k)
 {

@@ -22,6 +22,9 @@
  *   v3o_linear_row_f16       <- src/compute/kernels.rs:3630-3640 (linear_projection_f32_to_f32)
  *   v3o_mxfp4_*              <- cuda/src/kernels.cu:438-441 (E2M1 table), :2770-2777 (E8M0)
  *   v3o_fp4_quantize_act     <- cuda/src/kernels.cu:3193-3240 (+ compute_e8m0 :2759-2768)
+ *   v3o_fused_rms_norm_quantize_fp4, v3o_fp4_norm_inv
+ *                            <- cuda/src/kernels.cu:6585-6702 (sum order kept; rsqrtf replaced
+ *                               by the correctly rounded 1 / sqrtf)
  *   v3o_nvfp4_matvec         <- cuda/src/kernels.cu:5357-5449 (tiled split-half MMA GEMV)
  *   v3o_moe_experts_fused    <- cuda/src/kernels.cu:5650-5834, :5868-5990 (fused NVFP4 MoE)
  *   v3o_fp4_split_half / v3o_fp4_to_tiled <- cuda/src/kernels.cu:4132-4160, :4190-4225
@@ -157,6 +160,9 @@ uint8_t v3o_e2m1_rne(float v);
 float v3o_exp_cw(float x);
 /* x[k] f32 -> codes[ceil(k/32) * 16] split-half, scales[ceil(k/32)] E8M0 */
 void v3o_fp4_quantize_act(const float *x, size_t k, uint8_t *codes, uint8_t *scales);
+float v3o_fp4_norm_inv(const float *x, size_t k, float eps);
+void v3o_fused_rms_norm_quantize_fp4(const float *x, const uint16_t *w_f16, size_t k, float eps,
+                                     uint8_t *codes, uint8_t *scales, uint16_t *f16_out);
 /* out[m] = f32(exact sum over k of W[r][k] * a[k]); data tiled, scales [m][k/32] 2-byte */
 void v3o_nvfp4_matvec(const uint8_t *act_codes, const uint8_t *act_scales, const uint8_t *data,
                       const uint16_t *scales, size_t m, size_t k, float *out);

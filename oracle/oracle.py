@@ -52,6 +52,8 @@ def _declare(L: C.CDLL) -> None:
         "v3o_e2m1_rne": (C.c_uint8, [F]),
         "v3o_exp_cw": (F, [F]),
         "v3o_fp4_quantize_act": (None, [P, S, P, P]),
+        "v3o_fp4_norm_inv": (F, [P, S, F]),
+        "v3o_fused_rms_norm_quantize_fp4": (None, [P, P, S, F, P, P, P]),
         "v3o_nvfp4_matvec": (None, [P, P, P, P, S, S, P]),
         "v3o_moe_experts_fused": (None, [P, P, P, P, P, S, S, S, S, P]),
         "v3o_fp4_split_half": (None, [P, S]),
@@ -365,6 +367,25 @@ def fp4_quantize_act(x) -> tuple:
     sc = np.zeros(g, dtype=np.uint8)
     lib().v3o_fp4_quantize_act(_p(x), x.size, _p(codes), _p(sc))
     return codes, sc
+
+
+def fp4_norm_inv(x, eps) -> float:
+    """Inverse RMS in the order of kernels.cu:6610-6645 (correctly rounded 1/sqrt)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return float(np.float32(lib().v3o_fp4_norm_inv(_p(x), x.size, float(eps))))
+
+
+def fused_rms_norm_quantize_fp4(x, w_f16_bits, eps, f16_out=False) -> tuple:
+    """kernels.cu:6585 fused RMSNorm + FP4 quantize: (codes, scales[, f16 bits of the norm])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w_f16_bits, dtype=np.uint16)
+    g = (x.size + 31) // 32
+    codes = np.zeros(g * 16, dtype=np.uint8)
+    sc = np.zeros(g, dtype=np.uint8)
+    h = np.zeros(x.size, dtype=np.uint16) if f16_out else None
+    lib().v3o_fused_rms_norm_quantize_fp4(_p(x), _p(w), x.size, float(eps), _p(codes), _p(sc),
+                                          _p(h) if f16_out else None)
+    return (codes, sc, h) if f16_out else (codes, sc)
 
 
 def nvfp4_matvec(act_codes, act_scales, data, scales, m, k) -> np.ndarray:

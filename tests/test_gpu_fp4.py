@@ -260,3 +260,44 @@ def test_fused_gpu_graph_replay():
         ref = lay.oracle(rc, rs, ii, wi, np.zeros(m_out, np.float32))
         assert np.array_equal(got, ref)
     del graph
+
+
+@pytest.mark.parametrize("k,sigma,f16", [(7168, 20.0, True), (7168, 1.0, False), (3072, 5.0, True),
+                                         (96, 0.5, True), (9216, 2.0, False)])
+def test_fused_rms_norm_quantize_bit_exact(k, sigma, f16):
+    """kernels.cu:6585 fused RMSNorm + FP4 quantize (vib3_launch_fused_rms_norm_quantize_fp4):
+    codes, scales and the optional f16 output equal the oracle's bit for bit, for a residual-
+    stream magnitude, unit and small inputs, one workgroup (k = 96) and k above the single-load
+    form (9216)."""
+    from vib3_amd import kernels as K
+    _say(f"case: fused rms norm + fp4 quantize k={k} sigma={sigma} f16={f16}")
+    rng = np.random.default_rng(k + int(sigma))
+    x = rng.normal(0, sigma, k).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float16)
+    xd = torch.from_numpy(x).cuda()
+    wd = torch.from_numpy(w).cuda()
+    codes = torch.zeros(k // 2, dtype=torch.uint8, device="cuda")
+    sc = torch.zeros(k // 32, dtype=torch.uint8, device="cuda")
+    h = torch.zeros(k, dtype=torch.float16, device="cuda") if f16 else None
+    K.fused_rms_norm_quantize_fp4(xd, wd, codes, sc, h, k, 1e-6)
+    torch.cuda.synchronize()
+    ref = O.fused_rms_norm_quantize_fp4(x, w.view(np.uint16), 1e-6, f16_out=f16)
+    assert np.array_equal(codes.cpu().numpy(), ref[0])
+    assert np.array_equal(sc.cpu().numpy(), ref[1])
+    if f16:
+        assert np.array_equal(h.cpu().numpy().view(np.uint16), ref[2])
+
+
+def test_fused_rms_norm_quantize_errors():
+    from vib3_amd import _lib
+    lib = _lib.load()
+    x = torch.zeros(64, dtype=torch.float32, device="cuda")
+    w = torch.zeros(64, dtype=torch.float16, device="cuda")
+    c = torch.zeros(32, dtype=torch.uint8, device="cuda")
+    s = torch.zeros(2, dtype=torch.uint8, device="cuda")
+    f = lib.vib3_launch_fused_rms_norm_quantize_fp4
+    assert f(x.data_ptr(), w.data_ptr(), c.data_ptr(), s.data_ptr(), None, 0, 1e-6, _st()) != 0
+    assert f(x.data_ptr(), w.data_ptr(), c.data_ptr(), s.data_ptr(), None, 48, 1e-6, _st()) != 0
+    assert f(None, w.data_ptr(), c.data_ptr(), s.data_ptr(), None, 64, 1e-6, _st()) != 0
+    assert f(x.data_ptr(), w.data_ptr(), c.data_ptr(), s.data_ptr(), None, 64, 1e-6, _st()) == 0
+    torch.cuda.synchronize()

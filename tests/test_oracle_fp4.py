@@ -191,3 +191,36 @@ def test_repack_split_half_and_tiled_layouts():
         for t in range(nkt):
             off = (r // 16 * nkt + t) * 512 + (r % 16) * 32
             assert np.array_equal(tiled[off:off + 32], row[r * k // 2 + t * 32: r * k // 2 + t * 32 + 32])
+
+
+@pytest.mark.parametrize("k,sigma,eps", [(7168, 20.0, 1e-6), (3072, 1.0, 1e-5), (96, 1e-4, 1e-6)])
+def test_fp4_norm_inverse_rms_closed_form(k, sigma, eps):
+    """The fused norm's inverse RMS (kernels.cu:6610-6645 order) within 2 ulp of the float64
+    closed form 1 / sqrt(mean(x^2) + eps) at residual-stream, unit and eps-dominated
+    magnitudes (a dropped eps, a divide by k - 1 or a missing square fails it)."""
+    rng = np.random.default_rng(k)
+    x = rng.normal(0, sigma, k).astype(np.float32)
+    got = np.float32(O.fp4_norm_inv(x, eps))
+    want = 1.0 / np.sqrt(np.mean(x.astype(np.float64) ** 2) + eps)
+    assert abs(float(got) - want) <= 2 * float(np.spacing(np.float32(want)))
+
+
+def test_fused_rms_norm_quantize_known_answer_and_composition():
+    """All-ones activation and weights: y = 1/sqrt(1 + eps) ~ 1, so every group gets the
+    reference quantizer's all-1.0 answer (scale byte 125, codes 0x66, kernels.cu:2786-2797);
+    and in general the fused call equals the norm followed by the standalone quantizer, with
+    the f16 output the round-to-nearest-even of the normalised values."""
+    k = 256
+    codes, sc, h = O.fused_rms_norm_quantize_fp4(np.ones(k, np.float32),
+                                                 np.full(k, 0x3C00, np.uint16), 1e-6, f16_out=True)
+    assert codes.tolist() == [0x66] * (k // 2) and sc.tolist() == [125] * (k // 32)
+    assert np.all(h == np.float16(1.0 / np.sqrt(1 + 1e-6)).view(np.uint16))
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 7, 2048).astype(np.float32)
+    w = (1 + 0.2 * rng.standard_normal(2048)).astype(np.float16)
+    inv = np.float32(O.fp4_norm_inv(x, 1e-6))
+    y = (x * inv).astype(np.float32) * w.astype(np.float32)
+    c2, s2 = O.fp4_quantize_act(y.astype(np.float32))
+    c1, s1, h1 = O.fused_rms_norm_quantize_fp4(x, w.view(np.uint16), 1e-6, f16_out=True)
+    assert np.array_equal(c1, c2) and np.array_equal(s1, s2)
+    assert np.array_equal(h1, y.astype(np.float16).view(np.uint16))

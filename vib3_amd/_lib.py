@@ -116,6 +116,7 @@ SIGNATURES = {
     "vib3_build_page_table": (I, [P, C.c_uint16, P, I, P, P, P, I, P, P]),
     "vib3_build_page_table_resolved": (I, [P, S, P, I, P, P, P, I, P, P, I, P]),
     "vib3_launch_quantize_activation_fp4": (I, [P, P, P, I, P]),
+    "vib3_launch_fused_rms_norm_quantize_fp4": (I, [P, P, P, P, P, I, F, P]),
     "vib3_launch_quantize_activation_fp4_fast": (I, [P, P, P, I, P]),
     "vib3_moe_prewarm_gpu_bufs": (I, [I, I]),
     "vib3_launch_moe_experts_fused": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, P, P]),

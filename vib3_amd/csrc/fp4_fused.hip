@@ -353,6 +353,58 @@ __global__ __launch_bounds__(256) void k_fp4_quant_act(const float* x, uint8_t* 
   if (j == 0 && g * 32 < K) scales[g] = (uint8_t)e;
 }
 
+// Fused RMSNorm + FP4 quantizer (kernels.cu:6585-6702). Every workgroup forms the inverse RMS
+// in the reference's order: thread t accumulates x[d]^2 (fused multiply-adds) for d = t + 256 i,
+// each 32-thread half-wave sums by the butterfly xor 16 .. 1, and the eight half-wave sums
+// are added in order from 0; inv = 1 / sqrtf(ss / K + eps), correctly rounded (the reference
+// uses CUDA's approximate rsqrtf). Workgroup b then normalises and quantizes elements
+// [1024 b, 1024 b + 1024): y = (x * inv) * w, one lane per value as k_fp4_quant_act, and
+// optionally writes y as f16.
+__global__ __launch_bounds__(256) void k_fp4_rms_quant(const float* x, const uint16_t* w,
+                                                       uint8_t* codes, uint8_t* scales,
+                                                       uint16_t* f16_out, int K, float eps) {
+  __shared__ float ws[8];
+  const int tid = (int)threadIdx.x, lane = lane_id();
+  float p = 0.0f;
+  if (K <= 256 * 32) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) v[i] = tid + 256 * i < K ? x[tid + 256 * i] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) p = tid + 256 * i < K ? __builtin_fmaf(v[i], v[i], p) : p;
+  } else {
+    for (int d = tid; d < K; d += 256) p = __builtin_fmaf(x[d], x[d], p);
+  }
+#pragma unroll
+  for (int m = 16; m > 0; m >>= 1) p += __shfl_xor(p, m);
+  if ((tid & 31) == 0) ws[tid >> 5] = p;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) total += ws[i];
+  const float inv = 1.0f / __builtin_sqrtf(total / (float)K + eps);
+#pragma unroll
+  for (int it = 0; it < 4; it++) {
+    const int i = (int)blockIdx.x * 1024 + it * 256 + tid;
+    float y = 0.0f;
+    if (i < K) {
+#pragma clang fp contract(off)
+      y = x[i] * inv * f16_to_f32(w[i]);
+      if (f16_out) f16_out[i] = f32_to_f16_bits(y);
+    }
+    float amax = fabsf(y);
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+    const uint32_t e = e8m0_of_amax(amax);
+    const float is = amax == 0.0f ? 0.0f : e8m0_inv(e);
+    const uint32_t code = e2m1_rne(y * is);
+    const uint32_t hi = (uint32_t)__shfl(code, (lane & ~31) + (lane & 15) + 16);
+    const int g = i >> 5, j = i & 31;
+    if (j < 16 && i < K) codes[(size_t)g * 16 + j] = (uint8_t)(code | (hi << 4));
+    if (j == 0 && i < K) scales[g] = (uint8_t)e;
+  }
+}
+
 // Gate/up of every active expert + SwiGLU + FP4 quantization of h (kernels.cu:5357-5517 fused):
 // workgroup (q, s) = 32 rows [32q, 32q + 32) of slot s; wave w takes row block 2q + (w >> 2)
 // and k quarter w & 3 of both matrices; the quarters meet in LDS, and the 32 rows, one E8M0
@@ -618,6 +670,18 @@ int vib3_launch_quantize_activation_fp4(const void* input, void* act_fp4, void* 
   hipLaunchKernelGGL(k_fp4_quant_act, dim3((unsigned)((groups * 32 + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, (const float*)input, (uint8_t*)act_fp4,
                      (uint8_t*)act_scales, K);
+  VIB3_RETURN_LAUNCH();
+}
+
+int vib3_launch_fused_rms_norm_quantize_fp4(const void* input, const void* norm_weight,
+                                            void* act_fp4, void* act_scales, void* opt_f16_out,
+                                            int K, float eps, void* stream) {
+  if (K <= 0) return VIB3_ERR_BAD_COUNT;
+  if (K % 32) return VIB3_ERR_UNSUPPORTED;
+  if (!input || !norm_weight || !act_fp4 || !act_scales) return VIB3_ERR_BAD_POINTER;
+  hipLaunchKernelGGL(k_fp4_rms_quant, dim3((unsigned)((K + 1023) / 1024)), dim3(256), 0,
+                     (hipStream_t)stream, (const float*)input, (const uint16_t*)norm_weight,
+                     (uint8_t*)act_fp4, (uint8_t*)act_scales, (uint16_t*)opt_f16_out, K, eps);
   VIB3_RETURN_LAUNCH();
 }
 

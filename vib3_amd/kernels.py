@@ -252,6 +252,21 @@ def quantize_activation_fp4(input: torch.Tensor, act_fp4: torch.Tensor, act_scal
 quantize_activation_fp4_fast = quantize_activation_fp4
 
 
+def fused_rms_norm_quantize_fp4(input: torch.Tensor, norm_weight: torch.Tensor,
+                                act_fp4: torch.Tensor, act_scales: torch.Tensor,
+                                opt_f16_out, k: int, eps: float) -> None:
+    """kernels.rs:1641 fused_rms_norm_quantize_fp4: RMSNorm of the f32 hidden state [k] with
+    f16 weights, then split-half E2M1 codes [k/2] + E8M0 scales [k/32]; opt_f16_out (an f16
+    tensor [k], or None) receives the normalised values."""
+    if input.dtype != torch.float32 or norm_weight.dtype != torch.float16:
+        raise TypeError("fused_rms_norm_quantize_fp4 takes an f32 input and f16 weights")
+    _lib.call("vib3_launch_fused_rms_norm_quantize_fp4", _dev(input, "input"),
+              _dev(norm_weight, "norm_weight"), _dev(act_fp4, "act_fp4"),
+              _dev(act_scales, "act_scales"),
+              None if opt_f16_out is None else _dev(opt_f16_out, "opt_f16_out"), k, eps,
+              _stream(input))
+
+
 def moe_prewarm_gpu_bufs(m_mid: int, k_mid: int) -> None:
     """cuda_ffi.rs:1026 vib3_moe_prewarm_gpu_bufs: the fused MoE's intermediate buffer on the
     current device (the one allocation of this path; call before graph capture)."""
