@@ -333,6 +333,139 @@ __device__ __forceinline__ double shfl_xor_d(double v, int m) {
 
 // ------------------------------------------------------------------------- kernels
 
+// Down projection + weighted combine, one workgroup per CU: wave w owns the four output rows
+// 4 rg .. 4 rg + 3 (rg = the wave's row group) of every slot and walks the slots in order, so
+// each row's o = o + w_s * f32(d_s) is formed in registers in slot order (kernels.cu:5958-5990
+// accumulates the same terms). A step reads, for the wave's four rows, the 128 contiguous bytes
+// they hold in each of 8 J consecutive 512-byte tiles: lane l takes tiles (l >> 3) + 8 j, row
+// (l >> 1) & 3 and half l & 1, i.e. J 32-value groups, each reduced exactly (group_dot)
+// against the slot's staged intermediate and accumulated in f64 with its two E8M0 scales. The
+// slots' intermediates are staged in LDS once per workgroup; page addresses sit in lanes
+// (lane s: slot s). Needs M_mid % (512 J) == 0.
+#ifndef VIB3_FP4_DOWN_NB
+#define VIB3_FP4_DOWN_NB 2
+#endif
+
+template <int J>
+__global__ __launch_bounds__(1024) void k_fp4_down_rows(Fp4Args a) {
+  extern __shared__ uint4 lds[];
+  const int Gm = a.M_mid / 32, nkt = a.M_mid / 64, S8 = nkt / (8 * J), n = a.n;
+  uint4* hp = lds;                               // [n][Gm][4]
+  int* he = (int*)(lds + (size_t)n * Gm * 4);    // [n][Gm]
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int G4 = a.M_out / 4;
+  const int rg = (int)blockIdx.x * (int)(blockDim.x >> 6) + wave;
+  const int rgc = min(rg, G4 - 1);
+  const int rb = rgc >> 2, rs = rgc & 3;
+  const int t = lane >> 3, r = (lane >> 1) & 3, hh = lane & 1;
+  const int row = rb * 16 + rs * 4 + r;
+  // every slot's intermediate: loads first (thread-strided groups of all slots)
+  const int ngr = n * Gm;
+  uint4 hw[2];
+  uint8_t hx[2];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int g = min((int)threadIdx.x + u * (int)blockDim.x, ngr - 1), sl = g / Gm,
+              gi = g - sl * Gm;
+    const uint8_t* hc = a.mid + (size_t)sl * a.mid_stride;
+    hw[u] = *(const uint4*)(hc + (size_t)gi * 16);
+    hx[u] = hc[a.M_mid / 2 + gi];
+  }
+  // lane s < n: slot s's down page and routing weight; ok = 0 for an unusable slot
+  uint64_t my_d = 0, my_q = 0;
+  float my_w = 0.0f;
+  int my_ok = 0;
+  if (lane < n) {
+    const Fp4Mat m = slot_mat(a, lane, 2, a.M_out, a.M_mid);
+    if (m.data && m.scales) {
+      my_d = (uint64_t)(uintptr_t)m.data;
+      my_q = (uint64_t)(uintptr_t)m.scales;
+      my_ok = 1;
+      my_w = a.table ? a.wts_dev[lane] : a.wts[lane];
+    }
+  }
+  auto rl64 = [&](uint64_t v, int l) {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
+           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  };
+  const int total = n * S8;
+  struct Step {
+    uint4 w[J];
+    uint16_t q[J];
+  };
+  // step i = (slot i / S8, tiles (i % S8) 8 J ..); past the end or an unusable slot: the same
+  // loads from the intermediate buffer (no branch around the loads)
+  auto issue = [&](int i, Step& st) {
+    const int sl = min(i / S8, n - 1), s8 = i - (i / S8) * S8;
+    const bool ok = i < total && __builtin_amdgcn_readlane(my_ok, sl);
+    const uint8_t* d = (const uint8_t*)(uintptr_t)rl64(my_d, sl);
+    const uint16_t* qs = (const uint16_t*)(uintptr_t)rl64(my_q, sl);
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int kt = s8 * 8 * J + t + 8 * j;
+      const uint8_t* pw =
+          ok ? d + ((size_t)rb * nkt + kt) * 512 + (rs * 4 + r) * 32 + hh * 16 : a.mid;
+      const uint16_t* pq = ok ? qs + (size_t)row * Gm + 2 * kt + hh : (const uint16_t*)a.mid;
+      st.w[j] = ld_stream(pw);
+      st.q[j] = ld_u16(pq);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  constexpr int NB = VIB3_FP4_DOWN_NB;  // steps in the ring (NB - 1 in flight while one reduces)
+  Step bs[NB];
+#pragma unroll
+  for (int b = 0; b + 1 < NB; b++) issue(b, bs[b]);
+  // stage: the first two groups per thread from registers, the rest directly
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int g = (int)threadIdx.x + u * (int)blockDim.x;
+    if (g < ngr) {
+      const int sl = g / Gm, gi = g - sl * Gm;
+      Stage<1>::put(hp + (size_t)sl * Gm * 4, he + (size_t)sl * Gm, gi, hw[u], hx[u]);
+    }
+  }
+  for (int g = (int)threadIdx.x + 2 * (int)blockDim.x; g < ngr; g += (int)blockDim.x) {
+    const int sl = g / Gm, gi = g - sl * Gm;
+    const uint8_t* hc = a.mid + (size_t)sl * a.mid_stride;
+    Stage<1>::put(hp + (size_t)sl * Gm * 4, he + (size_t)sl * Gm, gi,
+                  *(const uint4*)(hc + (size_t)gi * 16), hc[a.M_mid / 2 + gi]);
+  }
+  __syncthreads();
+  if (rg >= G4) return;
+  float o = a.out[row];
+  double acc = 0.0;
+  for (int i = 0; i < total; i += NB) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      const int k = i + b;
+      VIB3_WAIT_VM((NB - 2) * 2 * J);  // step k's loads done
+      issue(k + NB - 1, bs[(b + NB - 1) % NB]);
+      const int sl = min(k / S8, n - 1), s8 = k - (k / S8) * S8;
+#pragma unroll
+      for (int j = 0; j < J; j++) {
+        const int g = 2 * (s8 * 8 * J + t + 8 * j) + hh;
+        const float sdot = group_dot(bs[b].w[j], hp + ((size_t)sl * Gm + g) * 4);
+        const int ew = (bs[b].q[j] >> 7) & 0xff;
+        const double tt = fma((double)sdot, pow2d(ew + he[sl * Gm + g] - 254), acc);
+        acc = k < total ? tt : acc;
+      }
+      if (s8 == S8 - 1 && k < total) {  // the slot's last step: its row sums, in order
+        double v = acc;
+        v += shfl_xor_d(v, 1);
+        v += shfl_xor_d(v, 8);
+        v += shfl_xor_d(v, 16);
+        v += shfl_xor_d(v, 32);
+        const float wsl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), sl));
+        const float nv = add_mul_rn(o, wsl, (float)v);
+        o = __builtin_amdgcn_readlane(my_ok, sl) ? nv : o;
+        acc = 0.0;
+      }
+    }
+  }
+  if (t == 0 && hh == 0) a.out[row] = o;
+}
+
 // Activation quantizer (kernels.cu:3193-3240): per group of 32, E8M0 from the absolute maximum,
 // values times 1/scale rounded to E2M1, packed split-half. One lane per value: each 32-lane
 // half of a wave is one group; lane j < 16 of the group writes byte j = code j | code j+16.
@@ -649,8 +782,20 @@ int launch_fused(Fp4Args& a, hipStream_t st) {
   a.mid_stride = mb.stride;
   hipLaunchKernelGGL(k_fp4_gateup, dim3((unsigned)(a.M_mid / 32), (unsigned)a.n), dim3(512),
                      (unsigned)gateup_lds(a.K_in), st, a);
-  hipLaunchKernelGGL(k_fp4_down, dim3((unsigned)(a.M_out / 16)), dim3(64 * a.n),
-                     (unsigned)down_lds(a.n, a.M_mid), st, a);
+  if (a.M_mid % 512 == 0 && getenv("VIB3_FP4_DOWN_BLOCKS") == nullptr) {
+    // one workgroup per CU, waves owning four output rows each
+    const int G4 = a.M_out / 4;
+    int wpb = (G4 + device_cus() - 1) / device_cus();
+    wpb = wpb < 1 ? 1 : wpb > 16 ? 16 : wpb;
+    const dim3 grid((unsigned)((G4 + wpb - 1) / wpb)), block(64 * wpb);
+    const unsigned lds = (unsigned)((size_t)a.n * (a.M_mid / 32) * 68);
+    if (a.M_mid % 2048 == 0) hipLaunchKernelGGL(k_fp4_down_rows<4>, grid, block, lds, st, a);
+    else if (a.M_mid % 1024 == 0) hipLaunchKernelGGL(k_fp4_down_rows<2>, grid, block, lds, st, a);
+    else hipLaunchKernelGGL(k_fp4_down_rows<1>, grid, block, lds, st, a);
+  } else {
+    hipLaunchKernelGGL(k_fp4_down, dim3((unsigned)(a.M_out / 16)), dim3(64 * a.n),
+                       (unsigned)down_lds(a.n, a.M_mid), st, a);
+  }
   VIB3_RETURN_LAUNCH();
 }
 
