@@ -353,8 +353,8 @@ def bench_fp4(args, cfg) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--layers", type=int, default=0, help="layers to rotate (default per config)")
     ap.add_argument("--tokens", type=int, default=64)
