@@ -168,6 +168,10 @@ LayerWs layer_ws(const vib3_moe_int4_layer* L, bool scratch = false) {
 
 }  // namespace
 
+#ifndef VIB3_DOWN_LIST
+#define VIB3_DOWN_LIST 1  // (build-time switch: the gate/up kernel lists the down pages)
+#endif
+
 extern "C" {
 
 const char* vib3_hip_version(void) { return "vib3_hip 0.1 gfx950"; }
@@ -495,7 +499,8 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only,
   }
   // the gate/up kernel lists the down page addresses for the down kernel (a down stage alone
   // reads the list its gate/up stage left, like h and the ids)
-  const bool bases = w.down_pages > 0 && w.down_pages <= L->max_pages && rows_write_bases(a);
+  const bool bases = VIB3_DOWN_LIST && w.down_pages > 0 && w.down_pages <= L->max_pages &&
+                     rows_write_bases(a);
   if (bases) {
     a.down_bases = (uint64_t*)(ws + w.dbase);
     a.down_pages = w.down_pages;

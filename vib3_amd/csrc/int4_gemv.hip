@@ -189,7 +189,8 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, size_t o, float v) 
 
 
 #ifndef VIB3_X_SHARED
-#define VIB3_X_SHARED 1  // (build-time switch: one wave converts the activations for all four)
+#define VIB3_X_SHARED 2  // (build-time switch: one wave converts the activations for all four;
+                         // 2 = only for f32 activations)
 #endif
 
 template <int NCH, bool DUAL, int XM, bool PAGED>
@@ -407,6 +408,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // converts them and the others copy them from LDS after the barrier below (a quarter of
   // the cache traffic, and none of it ahead of the selecting wave's polls).
   constexpr int XQ = XM == kXi16n ? kXi16 : XM;
+  constexpr bool XSH = VIB3_X_SHARED == 1 || (VIB3_X_SHARED == 2 && XM != kXf16);
   constexpr int XLW = XQ == kXsplit ? 17 : XQ == kXi16 ? 1 : 0;  // words of xl kept
   __shared__ uint32_t s_x[NCH * (17 + XLW) * kWave];
   auto copy_x = [&]() {  // this wave's chunks from the second wave's LDS copy
@@ -422,7 +424,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
       xl[j] = __builtin_bit_cast(XChunk, lw);
     }
   };
-  if (!VIB3_X_SHARED || wave == 1) {
+  if (!XSH || wave == 1) {
     load_x<NCH, XM>(a.x, a.x_dt, cpr, cidx, xh, xl, a.norm_w, inv);
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
@@ -435,7 +437,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
         s_x[(j * (17 + XLW) + 17 + k) * kWave + lane] = lw.w[XLW == 1 ? 16 : k];
     }
     // waves that stream shared items before the barrier take the copy once this flag is set
-    if (VIB3_X_SHARED && a.pre_shared) {
+    if (XSH && a.pre_shared) {
       wait_lgkm();
       if (lane == 0) __hip_atomic_store(&s_xready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
@@ -463,7 +465,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     VIB3_TRACE_POINT(2);
   }
   if (pre && cs > 0) {
-    if (VIB3_X_SHARED && wave != 1) {  // (the second wave sets the flag without waiting)
+    if (XSH && wave != 1) {  // (the second wave sets the flag without waiting)
       while (__hip_atomic_load(&s_xready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
         __builtin_amdgcn_s_sleep(1);
       copy_x();
@@ -490,25 +492,38 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   }
   __syncthreads();
   VIB3_TRACE_POINT(3);
-  if (VIB3_X_SHARED && wave != 1 && !(pre && cs > 0)) copy_x();
-  // block 0's first wave: the down segment's page addresses of every slot, for the down
-  // kernel (one table round trip there less)
-  if (PAGED && a.down_bases && blockIdx.x == 0 && wave == 0) {
-    typedef __attribute__((address_space(1))) const uint64_t gtab;
-    for (int i = lane; i < a.nslots * a.down_pages; i += kWave) {
-      const int sl = i / a.down_pages, p = i - sl * a.down_pages;
-      const uint64_t* t =
-          sl < top_k ? a.routed_table + ((size_t)s_sel[sl] * 3 + 2) * a.max_pages
-                     : a.shared_table + ((size_t)(sl - top_k) * 3 + 2) * a.max_pages;
-      a.down_bases[i] = *(gtab*)(t + p);
-    }
+  if (XSH && wave != 1 && !(pre && cs > 0)) copy_x();
+  // The down segment's page addresses of every slot, for the down kernel (one table round
+  // trip there less): wave 0 of workgroup b reads entries 64 b + lane (+ 64 G ...) of the
+  // [slot][page] list. The first entry's load goes out beside the wave's first item and is
+  // stored after the loop, so it costs no wait of its own.
+  typedef __attribute__((address_space(1))) const uint64_t gtab;
+  const int npl = PAGED && a.down_bases ? a.nslots * a.down_pages : 0;
+  auto pl_entry = [&](int i) {
+    const int sl = i / a.down_pages, p = i - sl * a.down_pages;
+    const uint64_t* t = sl < top_k ? a.routed_table + ((size_t)s_sel[sl] * 3 + 2) * a.max_pages
+                                   : a.shared_table + ((size_t)(sl - top_k) * 3 + 2) * a.max_pages;
+    return t + p;
+  };
+  const int pl_i = wave == 0 ? (int)blockIdx.x * kWave + lane : npl;
+  uint64_t pl_v = 0;
+  if (pl_i < npl) {
+    for (int i = pl_i + G * kWave; i < npl; i += G * kWave) a.down_bases[i] = *(gtab*)pl_entry(i);
+    pl_v = *(gtab*)pl_entry(pl_i);
   }
-  if (!have) return;
+  auto pl_store = [&]() {
+    if (pl_i < npl) a.down_bases[pl_i] = pl_v;
+  };
+  if (!have) {
+    pl_store();
+    return;
+  }
   if (item_at(cs) >= items) {  // shared items only: store them
     if (lane < kres) {
       const int item = item_at(lane), q = item / M;
       store_out(a, (size_t)slot_of(q) * a.out_stride + (item - q * M), res);
     }
+    pl_store();
     return;
   }
   if (PAGED) {
@@ -549,6 +564,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     const int q = item / M;
     store_out(a, (size_t)slot_of(q) * a.out_stride + (item - q * M), res);
   }
+  pl_store();
   VIB3_TRACE_POINT(4);
 }
 
