@@ -332,7 +332,10 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   RouterSegRaw<4> rrow;
   if (split_row) router_seg_issue<4, NORM>(a.router, (int)blockIdx.x, 0, 1, rrow, a.norm_w);
   VIB3_TRACE_POINT(11);  // router row issued
-  if (a.pre_shared) {  // (LDS holds whatever the CU's last workgroup left)
+  // one wave converts the activations for the workgroup (through LDS) for f32 activations;
+  // with f16 / bf16 (an exact permutation) every wave converts its own (measured faster)
+  constexpr bool XSH = VIB3_X_SHARED == 1 || (VIB3_X_SHARED == 2 && XM != kXf16);
+  if (XSH && a.pre_shared) {  // (LDS holds whatever the CU's last workgroup left)
     if (threadIdx.x == 0) s_xready = 0;
     __syncthreads();
   }
@@ -408,7 +411,6 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // converts them and the others copy them from LDS after the barrier below (a quarter of
   // the cache traffic, and none of it ahead of the selecting wave's polls).
   constexpr int XQ = XM == kXi16n ? kXi16 : XM;
-  constexpr bool XSH = VIB3_X_SHARED == 1 || (VIB3_X_SHARED == 2 && XM != kXf16);
   constexpr int XLW = XQ == kXsplit ? 17 : XQ == kXi16 ? 1 : 0;  // words of xl kept
   __shared__ uint32_t s_x[NCH * (17 + XLW) * kWave];
   auto copy_x = [&]() {  // this wave's chunks from the second wave's LDS copy
