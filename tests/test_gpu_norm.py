@@ -221,3 +221,50 @@ def test_fused_prologue_equals_prologue_kernel(hidden, inter, E, k, ns, monkeypa
         monkeypatch.delenv("VIB3_PROLOGUE_KERNEL")
         assert np.array_equal(ids_f, ids_s)
         assert np.array_equal(fused.view(np.uint32), sep.view(np.uint32)), t
+
+
+def test_sublayer_graph_replay():
+    """The whole sublayer (fused RMSNorm and shared gates in the gate/up kernel, residual in the
+    down epilogue) captured once in a HIP graph and replayed for three tokens, with new x and
+    residual copied in between: every replay equals an eager launch of the same token bit for
+    bit, and the router status stays clean."""
+    from vib3_amd import moe
+    from vib3_amd._lib import DT_BF16, ROUTER_SIGMOID
+    _say("case: sublayer graph capture + replays")
+    hidden, ns = 1024, 2
+    sh = _shape(moe, DT_BF16, hidden, 256, 16, ns)
+    bank = moe.Int4ExpertBank(sh, layer=6, seed=SEED)
+    w, bias = moe.make_router(sh, 6, SEED, 0.02, 0.1)
+    kw = dict(top_k=4, scoring_mode=ROUTER_SIGMOID, scaling_factor=2.827, normalize=True,
+              norm_weight=_dev16(_f16(hidden, 10, 0.1, 1.0)), norm_eps=1e-6,
+              shared_gate=_dev16(_f16(ns * hidden, 11, 0.02)))
+    layer = moe.MoeInt4Layer(bank, w, bias, **kw)
+    eager = moe.MoeInt4Layer(bank, w, bias, **kw)
+    xbuf = torch.from_numpy(_f32(hidden, 40, 20.0)).cuda()
+    rbuf = torch.from_numpy(_f32(hidden, 41, 20.0)).cuda()
+    side = torch.cuda.Stream()
+    layer.launch(xbuf, residual=rbuf)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        layer.launch(xbuf, residual=rbuf, stream=side)
+    torch.cuda.synchronize()
+    seen = set()
+    for t in range(3):
+        xt = torch.from_numpy(_f32(hidden, 50 + t, 20.0)).cuda()
+        rt = torch.from_numpy(_f32(hidden, 60 + t, 20.0)).cuda()
+        xbuf.copy_(xt)
+        rbuf.copy_(rt)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = layer.out.cpu().numpy().copy()
+        ids = tuple(layer.ids.cpu().numpy().tolist())
+        ref = eager.launch(xt, residual=rt).cpu().numpy().copy()
+        _say(f"  replay {t}")
+        assert ids == tuple(eager.ids.cpu().numpy().tolist())
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        seen.add(ids)
+    assert len(seen) > 1
+    assert layer.status() == 0
+    del graph
