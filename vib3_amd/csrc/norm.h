@@ -20,10 +20,17 @@ __device__ inline float block_inv_rms(float p, int D, float eps) {
   const int tid = (int)threadIdx.x;
   ss[tid] = p;
   __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (tid < s) ss[tid] += ss[tid + s];
-    __syncthreads();
+  if (tid < 128) ss[tid] += ss[tid + 128];
+  __syncthreads();
+  if (tid < 64) {
+    // the steps s = 64 .. 1 in the first wave's registers: lane t adds lane t + s, the same
+    // pairs as the tree in memory (lanes >= s compute values no later step reads)
+    float v = ss[tid] + ss[tid + 64];
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) v += __shfl_down(v, s);
+    if (tid == 0) ss[0] = v;
   }
+  __syncthreads();
   const float rms = sqrtf(ss[0] / (float)D + eps);
   const float inv = 1.0f / rms;
   __syncthreads();  // ss is reused by the next call
