@@ -58,12 +58,13 @@ def test_code_object_targets_gfx950(tmp_path):
 
 
 def test_integration_recipe_builds_a_complete_library(tmp_path):
-    """The build.rs recipe in INTEGRATION.md lists every translation unit build.py compiles,
+    """The integration guide's build.rs recipe lists every translation unit build.py compiles,
     and a library linked from exactly that list has no undefined vib3_* / launch_* symbol."""
     from vib3_amd import build
-    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    guide = os.path.join(ROOT, "INTEGRATION.md")
+    doc = open(guide).read()
     m = re.search(r"let src = \[([^\]]*)\];", doc)
-    assert m, "INTEGRATION.md has no `let src = [...]` line"
+    assert m, "the integration guide has no `let src = [...]` line"
     srcs = re.findall(r'"([^"]+)"', m.group(1))
     assert srcs == build.SOURCES
     lib = build.build(sources=srcs, out=str(tmp_path / "libvib3_recipe.so"),
