@@ -19,6 +19,8 @@
 // so results differ from the sequential CPU sum only by the order of f32 additions.
 #include <hip/hip_ext.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -860,13 +862,48 @@ static void mx_launch_rows_one(const MxArgs& a, hipStream_t st) {
 // Row-path launches (one-token and two-token experts): K = the reduction length picks the
 // chunks per lane (K <= 8192).
 template <bool GATEUP>
-static void mx_launch_rows(const MxArgs& a, int K, hipStream_t st) {
+static void mx_launch_rows(const MxArgs& a, int K, hipStream_t st1, hipStream_t st2) {
   switch ((K / 32 + 63) / 64) {
-    case 1: mx_launch_rows_one<GATEUP, 1, 1>(a, st); mx_launch_rows_one<GATEUP, 1, 2>(a, st); break;
-    case 2: mx_launch_rows_one<GATEUP, 2, 1>(a, st); mx_launch_rows_one<GATEUP, 2, 2>(a, st); break;
-    case 3: mx_launch_rows_one<GATEUP, 3, 1>(a, st); mx_launch_rows_one<GATEUP, 3, 2>(a, st); break;
-    default: mx_launch_rows_one<GATEUP, 4, 1>(a, st); mx_launch_rows_one<GATEUP, 4, 2>(a, st); break;
+    case 1: mx_launch_rows_one<GATEUP, 1, 1>(a, st1); mx_launch_rows_one<GATEUP, 1, 2>(a, st2); break;
+    case 2: mx_launch_rows_one<GATEUP, 2, 1>(a, st1); mx_launch_rows_one<GATEUP, 2, 2>(a, st2); break;
+    case 3: mx_launch_rows_one<GATEUP, 3, 1>(a, st1); mx_launch_rows_one<GATEUP, 3, 2>(a, st2); break;
+    default: mx_launch_rows_one<GATEUP, 4, 1>(a, st1); mx_launch_rows_one<GATEUP, 4, 2>(a, st2); break;
   }
+}
+
+// The two paths are independent until the combine: the matrix-core launches (hot experts) run
+// on the caller's stream and the row-path launches (cold experts) on a second stream of the
+// library (one per device, default priority), forked after the grouping and joined before the
+// combine with events, so each path fills the other's ramps and tails. Enqueueing is
+// serialised by a lock (the side stream and its two events are shared by every call on that
+// device); under graph capture the fork and join become graph edges.
+struct MxSide {
+  hipStream_t st = nullptr, st2 = nullptr;  // one-token and two-token row paths
+  hipEvent_t fork = nullptr, join = nullptr, join2 = nullptr;
+  bool ok = false;
+};
+#ifndef VIB3_MX_THREE_STREAMS
+#define VIB3_MX_THREE_STREAMS 1  // (build-time switch: the two row paths on streams of their own)
+#endif
+constexpr bool kMxThreeStreams = VIB3_MX_THREE_STREAMS;
+static MxSide g_mx_side[64];
+static std::mutex g_mx_side_lock;
+
+static MxSide* mx_side() {  // called with the lock held
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  MxSide& s = g_mx_side[dev];
+  if (!s.ok) {
+    if (hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&s.st2, hipStreamNonBlocking) != hipSuccess)
+      return nullptr;
+    if (hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&s.join2, hipEventDisableTiming) != hipSuccess)
+      return nullptr;
+    s.ok = true;
+  }
+  return &s;
 }
 
 struct MxWs {
@@ -959,6 +996,23 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   a.h = (uint16_t*)(ws + w.h); a.d = (uint16_t*)(ws + w.d);
   a.hidden = B->hidden; a.inter = B->inter;
   const unsigned items = (unsigned)mx_max_items(B);
+  std::unique_lock<std::mutex> lock(g_mx_side_lock, std::defer_lock);
+  MxSide* side = nullptr;
+  if (!getenv("VIB3_MX_ONE_STREAM")) {
+    lock.lock();
+    side = mx_side();
+  }
+  hipStream_t rs = st, rs2 = st;  // the row paths' streams
+  if (side) {
+    hipError_t e = hipEventRecord(side->fork, st);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side->st, side->fork, 0);
+    if (e == hipSuccess && kMxThreeStreams) e = hipStreamWaitEvent(side->st2, side->fork, 0);
+    if (e != hipSuccess) return (int)e;
+    rs = side->st;
+    rs2 = kMxThreeStreams ? side->st2 : side->st;
+  }
+  mx_launch_rows<true>(a, B->hidden, rs, rs2);
+  mx_launch_rows<false>(a, B->inter, rs, rs2);
   // matrix-core path: activations staged in LDS when k is a multiple of the step, otherwise
   // registers-only with k split over the waves (gate/up) or whole (down)
   if (B->hidden % kMx2K == 0)
@@ -968,7 +1022,6 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   else
     hipLaunchKernelGGL((k_mx_gemm<true, 4>), dim3((unsigned)(B->inter / 32), items), dim3(256), 0,
                        st, a);
-  mx_launch_rows<true>(a, B->hidden, st);
   if (B->inter % kMx2KD == 0)
     hipLaunchKernelGGL((k_mx_gemm2<false, kMx2KD>), dim3((unsigned)(B->hidden / (16 * kMx2W)), items),
                        dim3(64 * kMx2W),
@@ -976,7 +1029,13 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   else
     hipLaunchKernelGGL((k_mx_gemm<false, 1>), dim3((unsigned)(B->hidden / 256), items), dim3(256),
                        0, st, a);
-  mx_launch_rows<false>(a, B->inter, st);
+  if (side) {
+    hipError_t e = hipEventRecord(side->join, rs);
+    if (e == hipSuccess) e = hipStreamWaitEvent(st, side->join, 0);
+    if (e == hipSuccess && kMxThreeStreams) e = hipEventRecord(side->join2, rs2);
+    if (e == hipSuccess && kMxThreeStreams) e = hipStreamWaitEvent(st, side->join2, 0);
+    if (e != hipSuccess) return (int)e;
+  }
   hipLaunchKernelGGL(k_mx_combine, dim3((unsigned)((B->hidden + 2047) / 2048), (unsigned)B->tokens),
                      dim3(256), 0, st, (const uint16_t*)a.d, B->weights, B->ids,
                      B->num_experts, (uint16_t*)B->out, B->hidden, B->top_k);
