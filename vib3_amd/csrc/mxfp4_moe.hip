@@ -691,7 +691,7 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
   __shared__ int off[kMaxExperts];
   __shared__ int part[1024], dpart[1024], ipart[1024], cpart[1024];
   static_assert(kMxColdMax == 2, "the row path lists one- and two-token experts");
-  __shared__ uint16_t sid[kMxMaxPicks];
+  __shared__ __attribute__((aligned(16))) uint16_t sid[kMxMaxPicks];
   const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
   for (int e = tid; e < a.E; e += nt) cnt[e] = 0;
   for (int p = tid; p < a.n; p += nt) sid[p] = a.ids[p];
@@ -781,12 +781,21 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
   }
 
   __syncthreads();
-  // entry position = expert offset + number of earlier picks of the same expert
+  // entry position = expert offset + number of earlier picks of the same expert (the earlier
+  // ids read eight at a time from the 16-byte aligned LDS copy, the last few one by one)
   for (int p = tid; p < a.n; p += nt) {
     const int e = sid[p];
     if (e >= a.E) continue;
     int rank = 0;
-    for (int q = 0; q < p; q++) rank += sid[q] == e;
+    const int p8 = p & ~7;
+    for (int q = 0; q < p8; q += 8) {
+      const uint4 v = *(const uint4*)(sid + q);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        rank += (int)((w[j] & 0xffffu) == (uint32_t)e) + (int)((w[j] >> 16) == (uint32_t)e);
+    }
+    for (int q = p8; q < p; q++) rank += sid[q] == e;
     a.ent_tok[off[e] + rank] = p / a.top_k;
     a.ent_slot[off[e] + rank] = p;
   }
