@@ -173,3 +173,53 @@ def test_argument_errors():
     d = b.desc(x, ids, w)
     d.ids = None
     assert lib.vib3_launch_moe_mxfp4_batched(d, st) == -3
+
+
+def test_graph_replay_equals_eager():
+    """The batched launch (grouping, then the one-token rows, two-token rows and matrix-core
+    chains on three streams, then the combine) captured in a HIP graph: the fork and join
+    become graph edges, and three replays with new activations, ids and weights each equal an
+    eager launch bit for bit."""
+    from vib3_amd.mxfp4 import MoeMxfp4Batch
+    _say("case: mxfp4 batch graph capture + replays")
+    hidden, inter, E, T, k = 512, 768, 12, 24, 4
+    bank = _bank(hidden, inter, E, layer=3)
+    rng = np.random.default_rng(9)
+
+    def picks():
+        ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.uint16)
+        ids[: T // 2, 0] = 5  # a hot expert (matrix-core path) beside one- and two-token ones
+        ids[: T // 2, 1:] = np.where(ids[: T // 2, 1:] == 5, 6, ids[: T // 2, 1:])
+        w = rng.random((T, k)).astype(np.float32)
+        return ids, w
+
+    g = MoeMxfp4Batch(bank, T, k)
+    ref = MoeMxfp4Batch(bank, T, k)
+    xb, _ = _x(T, hidden, 80)
+    xb = xb.clone()
+    ids0, w0 = picks()
+    ib = torch.from_numpy(ids0.view(np.int16)).cuda()
+    wb = torch.from_numpy(w0).cuda()
+    g.launch(xb, ib, wb)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        g.launch(xb, ib, wb)
+    torch.cuda.synchronize()
+    for r in range(3):
+        xt, _ = _x(T, hidden, 81 + r)
+        ids, w = picks()
+        xb.copy_(xt)
+        ib.copy_(torch.from_numpy(ids.view(np.int16)).cuda())
+        wb.copy_(torch.from_numpy(w).cuda())
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = g.out.view(torch.int16).cpu().numpy().copy()
+        want = ref.launch(xt, torch.from_numpy(ids.view(np.int16)).cuda(),
+                          torch.from_numpy(w).cuda())
+        torch.cuda.synchronize()
+        _say(f"  replay {r}")
+        assert np.array_equal(got, want.view(torch.int16).cpu().numpy())
+    del graph
