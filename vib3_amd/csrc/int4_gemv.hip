@@ -196,6 +196,29 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, size_t o, float v) 
 template <int NCH, bool DUAL, int XM, bool PAGED>
 __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   VIB3_TRACE_POINT(0);
+  // Fused routing: this workgroup's router row (blockIdx.x < E) is on every routed row's
+  // critical path, so its loads are the kernel's first, ahead of the item bookkeeping and its
+  // kernel-argument reads. Fused prologue (NORM): the residual stream in the norm's thread
+  // layout (x[t + 256 i]) goes out just before it; the launcher guarantees fused routing with
+  // every router row in the split form below, and K <= 256 * kNormMax.
+  if (PAGED)  // (the arguments that choose and address it, requested in one round trip)
+    asm volatile("" ::"s"(a.route), "s"(a.router.E), "s"(a.router.D), "s"(a.router.w),
+                 "s"(a.router.x), "s"(a.router.w_dt), "s"(a.router.x_dt));
+  const bool fused = PAGED && a.route == kRouteFused;
+  const int E = a.router.E, G = (int)gridDim.x;
+  constexpr bool NORM = XM == kXi16n;
+  float xr[NORM ? kNormMax : 1];
+  if (NORM) {
+#pragma unroll
+    for (int i = 0; i < kNormMax; i++) {
+      const int d = (int)threadIdx.x + 256 * i;
+      xr[i] = ((const float*)a.x)[d < a.K ? d : 0];
+    }
+  }
+  const bool split_row = fused & ((int)blockIdx.x < E) & router_seg_ok(a.router, 1, 4);
+  RouterSegRaw<4> rrow;
+  if (split_row) router_seg_issue<4, NORM>(a.router, (int)blockIdx.x, 0, 1, rrow, a.norm_w);
+  VIB3_TRACE_POINT(11);  // router row issued
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform (SGPR)
   const int pk = a.K / 2, ng = (a.K + a.g - 1) / a.g, cpr = a.K / 32;
@@ -306,8 +329,6 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // a router row starts its expert stream only after the selection, so the CU's memory
   // pipeline serves the router rows, which every routed row waits for, first. (Cutting rows
   // into halves to spread them evenly over the two workgroups of a CU measured slower.)
-  const bool fused = PAGED && a.route == kRouteFused;
-  const int E = a.router.E, G = (int)gridDim.x;
   auto publish = [&](int e, float v) {
     if (threadIdx.x == 0) {
       __hip_atomic_store(a.router.slots + e,
@@ -316,22 +337,6 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
       if (a.router.scores) a.router.scores[e] = v;
     }
   };
-  // Fused prologue (NORM): the residual stream in the norm's thread layout (x[t + 256 i]),
-  // issued first; the launcher guarantees fused routing with every router row in the split
-  // form below, and K <= 256 * kNormMax.
-  constexpr bool NORM = XM == kXi16n;
-  float xr[NORM ? kNormMax : 1];
-  if (NORM) {
-#pragma unroll
-    for (int i = 0; i < kNormMax; i++) {
-      const int d = (int)threadIdx.x + 256 * i;
-      xr[i] = ((const float*)a.x)[d < a.K ? d : 0];
-    }
-  }
-  const bool split_row = fused && (int)blockIdx.x < E && router_seg_ok(a.router, 1, 4);
-  RouterSegRaw<4> rrow;
-  if (split_row) router_seg_issue<4, NORM>(a.router, (int)blockIdx.x, 0, 1, rrow, a.norm_w);
-  VIB3_TRACE_POINT(11);  // router row issued
   // one wave converts the activations for the workgroup (through LDS) for f32 activations;
   // with f16 / bf16 (an exact permutation) every wave converts its own (measured faster)
   constexpr bool XSH = VIB3_X_SHARED == 1 || (VIB3_X_SHARED == 2 && XM != kXf16);

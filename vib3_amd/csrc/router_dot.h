@@ -100,9 +100,11 @@ struct RouterSegRaw {
   uint4 n[U];  // RMSNorm weights (f16) of the groups, when the norm is fused
 };
 
+// (Evaluated without short-circuits, so every argument it reads is loaded at once.)
 __device__ inline bool router_seg_ok(const RouterArgs& a, int parts, int U) {
-  return a.D % (8 * parts) == 0 && a.D / parts <= 8 * U * 256 && (((uintptr_t)a.w) & 15) == 0 &&
-         (((uintptr_t)a.x) & 15) == 0;
+  return (a.D % (8 * parts) == 0) & (a.D / parts <= 8 * U * 256) &
+         ((((uintptr_t)a.w | (uintptr_t)a.x) & 15) == 0) & ((unsigned)a.w_dt <= VIB3_DT_BF16) &
+         ((unsigned)a.x_dt <= VIB3_DT_BF16);
 }
 
 // NORM: x is the f32 residual stream and the dot product takes RMSNorm(x) (weights nw, the
