@@ -147,14 +147,17 @@ def test_fused_gpu_kimi_shape_bit_exact():
     assert np.array_equal(out2.cpu().numpy(), got)
 
 
-def test_fused_gpu_skips_unusable_slots_and_checks_arguments():
+@pytest.mark.parametrize("m_mid,odd_ids", [(256, False), (512, True)])
+def test_fused_gpu_skips_unusable_slots_and_checks_arguments(m_mid, odd_ids):
     """An id >= num_experts_total and an id whose table entry is 0 contribute nothing;
-    argument errors return the reference's codes (-2 more than 8 experts) or ours."""
+    argument errors return the reference's codes (-2 more than 8 experts) or ours. M_mid 512
+    takes the one-workgroup-per-CU down kernel (page addresses from the gate/up kernel's
+    records); odd_ids passes the ids at an address that is 2 mod 4."""
     from vib3_amd import _lib
     from vib3_amd import kernels as K
-    _say("case: fused_gpu unusable slots, errors")
+    _say(f"case: fused_gpu unusable slots, errors, m_mid {m_mid}, odd ids {odd_ids}")
     rng = np.random.default_rng(11)
-    k_in, m_mid, m_out, E = 512, 256, 256, 16
+    k_in, m_out, E = 512, 256, 16
     ids = np.array([3, 40, 9, 5], dtype=np.uint16)  # 40 >= E; 5 gets no pages below
     lay = Fp4Layer(rng, 1, E, 0, ids[:3], k_in, m_mid, m_out)
     wts = np.array([0.5, 9.0, -0.25, 7.0], np.float32)
@@ -162,7 +165,10 @@ def test_fused_gpu_skips_unusable_slots_and_checks_arguments():
     K.moe_prewarm_gpu_bufs(m_mid, m_mid)
     _, codes, sc = quantize_dev(x)
     out = torch.zeros(m_out, dtype=torch.float32, device="cuda")
-    K.moe_experts_fused_gpu(codes, sc, lay.table, torch.from_numpy(ids.view(np.int16)).cuda(),
+    ids_dev = torch.from_numpy(np.concatenate([[7], ids]).astype(np.uint16).view(np.int16)).cuda()
+    ids_dev = ids_dev[1:] if odd_ids else ids_dev[1:].clone()
+    assert (ids_dev.data_ptr() % 4 == 2) == odd_ids
+    K.moe_experts_fused_gpu(codes, sc, lay.table, ids_dev,
                             torch.from_numpy(wts).cuda(), 0, E, 4, k_in, m_mid, m_out, out)
     ref = lay.oracle(codes.cpu().numpy(), sc.cpu().numpy(), ids, wts,
                      np.zeros(m_out, np.float32))

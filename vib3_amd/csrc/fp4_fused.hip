@@ -159,10 +159,15 @@ struct Fp4Args {
   float wts[kFp4MaxActive];
   int n;                  // active experts
   int K_in, M_mid, M_out;
-  uint8_t* mid;           // per slot: [M_mid/2] codes, then [M_mid/32] E8M0 (stride mid_stride)
+  // per slot (stride mid_stride): [M_mid/2] codes, [M_mid/32] E8M0, and in the stride's last
+  // 16 bytes the slot's down record {data, scales} (both 0 for an unusable slot), written by
+  // the gate/up kernel so the down kernel reads its page addresses in one round trip
+  uint8_t* mid;
   size_t mid_stride;
   float* out;             // [M_out] += sum_e w_e * down_e(h_e)
 };
+
+constexpr int kDownRecord = 16;  // bytes of a slot's down record in the intermediate buffer
 
 // Matrix `seg` of slot s, or {null, null} when the slot's id or page is not usable.
 __device__ __forceinline__ Fp4Mat slot_mat(const Fp4Args& a, int s, int seg, int rows, int K) {
@@ -173,6 +178,29 @@ __device__ __forceinline__ Fp4Mat slot_mat(const Fp4Args& a, int s, int seg, int
   if (!page) return Fp4Mat{nullptr, nullptr};
   const uint8_t* p = (const uint8_t*)(uintptr_t)page;
   return Fp4Mat{p, (const uint16_t*)(p + (size_t)(K / 2) * rows)};
+}
+
+// The three matrices of slot s for a workgroup-uniform s, as slot_mat gives them: the id (the
+// aligned word that holds it) and the table row through scalar loads, one round trip each,
+// shared by the three.
+__device__ __forceinline__ void slot_mats(const Fp4Args& a, int s, Fp4Mat (&m)[3]) {
+  if (!a.table) {
+#pragma unroll
+    for (int g = 0; g < 3; g++) m[g] = a.mat[s][g];
+    return;
+  }
+  const uintptr_t pid = (uintptr_t)(a.ids + s);
+  const uint32_t w = *(const __attribute__((address_space(4))) uint32_t*)(pid & ~(uintptr_t)3);
+  const int id = (int)((pid & 2) ? (w >> 16) : (w & 0xffffu));
+  const uint64_t* row = a.table + ((size_t)a.layer * a.E + (id < a.E ? id : 0)) * 3;
+  const uint64_t pg[3] = {ld_table(row), ld_table(row + 1), ld_table(row + 2)};
+#pragma unroll
+  for (int g = 0; g < 3; g++) {
+    const int rows = g < 2 ? a.M_mid : a.M_out, K = g < 2 ? a.K_in : a.M_mid;
+    const uint8_t* p = (const uint8_t*)(uintptr_t)pg[g];
+    m[g] = id < a.E && pg[g] ? Fp4Mat{p, (const uint16_t*)(p + (size_t)(K / 2) * rows)}
+                             : Fp4Mat{nullptr, nullptr};
+  }
 }
 
 // Decode split-half groups (codes + E8M0 bytes) into LDS pairs and exponents: group g of
@@ -348,6 +376,10 @@ __device__ __forceinline__ double shfl_xor_d(double v, int m) {
 
 template <int J>
 __global__ __launch_bounds__(1024) void k_fp4_down_rows(Fp4Args a) {
+  VIB3_TRACE_POINT(0);
+  // the kernel arguments the prologue reads, requested together (one round trip)
+  asm volatile("" ::"s"(a.n), "s"(a.M_mid), "s"(a.M_out), "s"(a.mid), "s"(a.mid_stride),
+               "s"(a.table), "s"(a.wts_dev), "s"((int)blockDim.x));
   extern __shared__ uint4 lds[];
   const int Gm = a.M_mid / 32, nkt = a.M_mid / 64, S8 = nkt / (8 * J), n = a.n;
   uint4* hp = lds;                               // [n][Gm][4]
@@ -360,6 +392,13 @@ __global__ __launch_bounds__(1024) void k_fp4_down_rows(Fp4Args a) {
   const int rb = rgc >> 2, rs = rgc & 3;
   const int t = lane >> 3, r = (lane >> 1) & 3, hh = lane & 1;
   const int row = rb * 16 + rs * 4 + r;
+  // lane s < n: slot s's down record (data, scales; 0 for an unusable slot), first
+  uint64_t my_d = 0, my_q = 0;
+  if (lane < n) {
+    const uint4 rec = *(const uint4*)(a.mid + (size_t)(lane + 1) * a.mid_stride - kDownRecord);
+    my_d = ((uint64_t)rec.y << 32) | rec.x;
+    my_q = ((uint64_t)rec.w << 32) | rec.z;
+  }
   // every slot's intermediate: loads first (thread-strided groups of all slots)
   const int ngr = n * Gm;
   uint4 hw[2];
@@ -372,19 +411,10 @@ __global__ __launch_bounds__(1024) void k_fp4_down_rows(Fp4Args a) {
     hw[u] = *(const uint4*)(hc + (size_t)gi * 16);
     hx[u] = hc[a.M_mid / 2 + gi];
   }
-  // lane s < n: slot s's down page and routing weight; ok = 0 for an unusable slot
-  uint64_t my_d = 0, my_q = 0;
+  // lane s < n: slot s's routing weight; ok = 0 for an unusable slot
   float my_w = 0.0f;
-  int my_ok = 0;
-  if (lane < n) {
-    const Fp4Mat m = slot_mat(a, lane, 2, a.M_out, a.M_mid);
-    if (m.data && m.scales) {
-      my_d = (uint64_t)(uintptr_t)m.data;
-      my_q = (uint64_t)(uintptr_t)m.scales;
-      my_ok = 1;
-      my_w = a.table ? a.wts_dev[lane] : a.wts[lane];
-    }
-  }
+  if (lane < n) my_w = a.table ? a.wts_dev[lane] : a.wts[lane];
+  const int my_ok = (my_d != 0) & (my_q != 0);
   auto rl64 = [&](uint64_t v, int l) {
     return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
@@ -416,6 +446,13 @@ __global__ __launch_bounds__(1024) void k_fp4_down_rows(Fp4Args a) {
   Step bs[NB];
 #pragma unroll
   for (int b = 0; b + 1 < NB; b++) issue(b, bs[b]);
+  VIB3_TRACE_POINT(1);  // first steps issued
+  // Every lane takes delivery of its intermediate words here, outside the masked region below
+  // (a wait inside it would leave the compiler unsure whether they are done, and it would
+  // then wait for the weight loads as well).
+#pragma unroll
+  for (int u = 0; u < 2; u++)
+    asm volatile("" ::"v"(hw[u].x), "v"(hw[u].y), "v"(hw[u].z), "v"(hw[u].w), "v"((uint32_t)hx[u]));
   // stage: the first two groups per thread from registers, the rest directly
 #pragma unroll
   for (int u = 0; u < 2; u++) {
@@ -432,6 +469,7 @@ __global__ __launch_bounds__(1024) void k_fp4_down_rows(Fp4Args a) {
                   *(const uint4*)(hc + (size_t)gi * 16), hc[a.M_mid / 2 + gi]);
   }
   __syncthreads();
+  VIB3_TRACE_POINT(2);  // intermediates staged
   if (rg >= G4) return;
   float o = a.out[row];
   double acc = 0.0;
@@ -461,8 +499,12 @@ __global__ __launch_bounds__(1024) void k_fp4_down_rows(Fp4Args a) {
         o = __builtin_amdgcn_readlane(my_ok, sl) ? nv : o;
         acc = 0.0;
       }
+#ifdef VIB3_TRACE
+      if (k == 0) VIB3_TRACE_POINT(3);  // first step reduced
+#endif
     }
   }
+  VIB3_TRACE_POINT(4);  // loop end
   if (t == 0 && hh == 0) a.out[row] = o;
 }
 
@@ -552,13 +594,29 @@ __global__ __launch_bounds__(512) void k_fp4_gateup(Fp4Args a) {
   const int s = (int)blockIdx.y, q = (int)blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = lane_id();
-  const Fp4Mat up = slot_mat(a, s, 0, a.M_mid, a.K_in);
-  const Fp4Mat gate = slot_mat(a, s, 1, a.M_mid, a.K_in);
+  // the kernel arguments the prologue reads, requested together (one round trip)
+  asm volatile("" ::"s"(a.table), "s"(a.ids), "s"(a.E), "s"(a.layer), "s"(a.K_in), "s"(a.M_mid),
+               "s"(a.M_out), "s"(a.mid), "s"(a.mid_stride), "s"(a.act), "s"(a.act_sc),
+               "s"((int)blockDim.x));
+  Fp4Mat mats[3];
+  slot_mats(a, s, mats);
+  const Fp4Mat up = mats[0], gate = mats[1];
   uint8_t* hcodes = a.mid + (size_t)s * a.mid_stride;
   uint8_t* hsc = hcodes + a.M_mid / 2;
+  // workgroup (0, s) also writes slot s's down record (stored at its end: no wait for it here)
+  const Fp4Mat dn = mats[2];
+  auto put_record = [&]() {
+    if (q == 0 && threadIdx.x == 0) {
+      const bool ok = dn.data && dn.scales;
+      uint64_t* rec = (uint64_t*)(hcodes + a.mid_stride - kDownRecord);
+      rec[0] = ok ? (uint64_t)(uintptr_t)dn.data : 0;
+      rec[1] = ok ? (uint64_t)(uintptr_t)dn.scales : 0;
+    }
+  };
   if (!up.data || !gate.data || !up.scales || !gate.scales) {  // unusable slot: h = 0
     if (threadIdx.x < 16) hcodes[(size_t)q * 16 + threadIdx.x] = 0;
     if (threadIdx.x == 0) hsc[q] = 0;
+    put_record();
     return;
   }
   const int rb = 2 * q + (wave >> 2), kq = wave & 3;
@@ -613,6 +671,7 @@ __global__ __launch_bounds__(512) void k_fp4_gateup(Fp4Args a) {
     if (lane == 0) hsc[q] = (uint8_t)e;
     (void)hrow;
   }
+  put_record();
 }
 
 // Down of every active expert + weighted accumulate (kernels.cu:5519-5591): workgroup rb =
@@ -744,7 +803,10 @@ struct MidBuf {
 MidBuf g_mid[64];
 std::mutex g_mid_lock;
 
-size_t mid_stride(int m_mid) { return ((size_t)m_mid / 2 + (size_t)m_mid / 32 + 255) / 256 * 256; }
+// per slot: codes, E8M0 bytes, and at the end of the slot's stride the 16-byte down record
+size_t mid_stride(int m_mid) {
+  return ((size_t)m_mid / 2 + (size_t)m_mid / 32 + kDownRecord + 255) / 256 * 256;
+}
 
 int current_device() {
   int dev = 0;
@@ -940,3 +1002,11 @@ int vib3_launch_repack_row_to_tiled(void* weight_data_ptr, void* temp_buf, int M
 }
 
 }  // extern "C"
+
+#ifdef VIB3_TRACE
+// Profiling builds only: where this translation unit's kernels write their timeline probes.
+extern "C" int vib3_trace_set_fp4(void* buf) {
+  uint64_t* p = (uint64_t*)buf;
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(vib3_trace_buf), &p, sizeof(p));
+}
+#endif
