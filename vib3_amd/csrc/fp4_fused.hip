@@ -369,7 +369,7 @@ __device__ __forceinline__ double shfl_xor_d(double v, int m) {
 // (l >> 1) & 3 and half l & 1, i.e. J 32-value groups, each reduced exactly (group_dot)
 // against the slot's staged intermediate and accumulated in f64 with its two E8M0 scales. The
 // slots' intermediates are staged in LDS once per workgroup; page addresses sit in lanes
-// (lane s: slot s). Needs M_mid % (512 J) == 0.
+// (lane s: slot s, from the slot's down record). Needs M_mid % (512 J) == 0.
 #ifndef VIB3_FP4_DOWN_NB
 #define VIB3_FP4_DOWN_NB 2
 #endif
@@ -584,7 +584,21 @@ __global__ __launch_bounds__(256) void k_fp4_rms_quant(const float* x, const uin
 // workgroup (q, s) = 32 rows [32q, 32q + 32) of slot s; wave w takes row block 2q + (w >> 2)
 // and k quarter w & 3 of both matrices; the quarters meet in LDS, and the 32 rows, one E8M0
 // group of h, are quantized and written split-half.
+#ifdef VIB3_TRACE  // (2-D grid: one probe row per workgroup, y-major)
+#define FP4_TRACE(k)                                                                     \
+  do {                                                                                   \
+    if (threadIdx.x == 0)                                                                \
+      vib3_trace_buf[(blockIdx.y * gridDim.x + blockIdx.x) * 16 + (k)] =                 \
+          __builtin_amdgcn_s_memrealtime();                                              \
+  } while (0)
+#else
+#define FP4_TRACE(k) \
+  do {               \
+  } while (0)
+#endif
+
 __global__ __launch_bounds__(512) void k_fp4_gateup(Fp4Args a) {
+  FP4_TRACE(0);
   extern __shared__ uint4 lds[];
   const int Gin = a.K_in / 32, nkt = a.K_in / 64, P = nkt / 2;
   uint4* act_pairs = lds;                               // [Gin][4]
@@ -634,12 +648,15 @@ __global__ __launch_bounds__(512) void k_fp4_gateup(Fp4Args a) {
   st[1].issue_scales();
   st[0].start();  // unconditional (an empty range re-reads pair 0): the waits stay exact
   st[1].start();
+  FP4_TRACE(1);  // weight streams started
   stage.finish(act_pairs, act_exp);
   st[0].finish_scales();
   st[1].finish_scales();
   __syncthreads();
+  FP4_TRACE(2);  // activations and scales staged
   double acc[2] = {0.0, 0.0};
   if (p0 < p1) run_streams<kFp4Depth, 2>(st, act_pairs, act_exp, acc);
+  FP4_TRACE(3);  // (wave 0) streams done
   double u = acc[0], g = acc[1];
   u += shfl_xor_d(u, 16);
   g += shfl_xor_d(g, 16);
@@ -672,6 +689,7 @@ __global__ __launch_bounds__(512) void k_fp4_gateup(Fp4Args a) {
     (void)hrow;
   }
   put_record();
+  FP4_TRACE(4);
 }
 
 // Down of every active expert + weighted accumulate (kernels.cu:5519-5591): workgroup rb =
