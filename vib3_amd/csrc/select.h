@@ -8,6 +8,14 @@
 #include "common.h"
 #include "kernels.h"
 
+#ifdef VIB3_TRACE_SELECT  // (profiling builds: probes inside the selection too)
+#define VIB3_TRACE_FINE(k) VIB3_TRACE_POINT(k)
+#else
+#define VIB3_TRACE_FINE(k) \
+  do {                    \
+  } while (0)
+#endif
+
 namespace vib3 {
 
 // (key, index) arg-max over the wave: larger key wins, ties go to the lower index (the order
@@ -146,7 +154,7 @@ __device__ inline bool select_fast(const RouterArgs& a, const float (&key)[R],
 #pragma unroll
   for (int g = 0; g < kWave; g += 8)
     t = fminf(t, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), g)));
-  VIB3_TRACE_POINT(8);  // threshold
+  VIB3_TRACE_FINE(8);  // threshold
   int n = 0;
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -162,7 +170,7 @@ __device__ inline bool select_fast(const RouterArgs& a, const float (&key)[R],
     n += __popcll(mask);
   }
   VIB3_TRACE_VALUE(7, n);
-  VIB3_TRACE_POINT(9);  // compacted
+  VIB3_TRACE_FINE(9);  // compacted
   if (n > kWave) return false;
   if (lane >= n && lane < ((n + 7) & ~7)) {  // pad to a multiple of 8: never beats anything
     ck[lane] = -__builtin_huge_valf();
@@ -189,7 +197,7 @@ __device__ inline bool select_fast(const RouterArgs& a, const float (&key)[R],
     sel[rank] = mi;
     selv[rank] = mv;
   }
-  VIB3_TRACE_POINT(10);  // ranked
+  VIB3_TRACE_FINE(10);  // ranked
   wait_lgkm();
   __builtin_amdgcn_wave_barrier();
   return true;
@@ -225,7 +233,7 @@ __device__ inline void select_topk_vals(const RouterArgs& a, const float (&sc)[R
   }
   VIB3_TRACE_POINT(5);  // scores and bias in registers
   if (a.top_k <= 8 && select_fast<R>(a, key, val, idx, sel, selv)) {
-    VIB3_TRACE_POINT(6);  // picks done
+    VIB3_TRACE_FINE(6);  // picks done
     router_weights_wave(a, sel, selv, publish);
     wait_lgkm();
     __builtin_amdgcn_wave_barrier();
@@ -271,7 +279,7 @@ __device__ inline void select_topk_vals(const RouterArgs& a, const float (&sc)[R
   }
   wait_lgkm();
   __builtin_amdgcn_wave_barrier();
-  VIB3_TRACE_POINT(6);  // picks done
+  VIB3_TRACE_FINE(6);  // picks done
   router_weights_wave(a, sel, selv, publish);
   wait_lgkm();
   __builtin_amdgcn_wave_barrier();
