@@ -173,6 +173,15 @@ def test_fused_gpu_skips_unusable_slots_and_checks_arguments(m_mid, odd_ids):
     ref = lay.oracle(codes.cpu().numpy(), sc.cpu().numpy(), ids, wts,
                      np.zeros(m_out, np.float32))
     assert np.array_equal(out.cpu().numpy(), ref)
+    # the host-pointer entry point: an expert whose pages are null contributes nothing either
+    pages = [(int(lay.table_host[0, e][0]), int(lay.table_host[0, e][1]),
+              int(lay.table_host[0, e][2]), float(w)) for e, w in zip(ids[[0, 2]], wts[[0, 2]])]
+    pages.insert(1, (0, 0, 0, 9.0))
+    out_h = torch.zeros(m_out, dtype=torch.float32, device="cuda")
+    K.moe_experts_fused(codes, sc, pages, k_in, m_mid, m_out, out_h)
+    ref_h = lay.oracle(codes.cpu().numpy(), sc.cpu().numpy(), ids[:3], wts[:3],
+                       np.zeros(m_out, np.float32))
+    assert np.array_equal(out_h.cpu().numpy(), ref_h)
     lib = _lib.load()
     args = lambda n, ki, mm, km, mo: (codes.data_ptr(), sc.data_ptr(), lay.table.data_ptr(),
                                       0, 0, 0, E, n, ki, mm, km, mo, out.data_ptr(), _st())
