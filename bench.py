@@ -536,7 +536,8 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4 weights x bf16 activations, f32 accumulate",
+        "dtype": f"int4 weights x {'f32' if args.sublayer else cfg['x_dtype']} activations, "
+                 "f32 accumulate",
         "data": "synthetic (counter-based generator; random-init weights of the named shape)",
         "config": {"workload": cfg["workload"] + ("; whole sublayer: f32 residual stream in, "
                                                   "RMSNorm, sigmoid-gated shared expert, "
@@ -544,8 +545,8 @@ def main() -> int:
                    "layers_rotated": L, "tokens": args.tokens,
                    "layout": cfg["layout"], "algorithmic_bytes_per_layer": nbytes["layer"]},
         "roofline": {"bound": "hbm",
-                     "kernel": "k_int4_rows<4,true> (router logits + top-k + gate/up GEMV + SwiGLU)"
-                               if fused else "k_int4_rows<4,true> (top-k + gate/up GEMV + SwiGLU)",
+                     "kernel": "k_int4_rows (router logits + top-k + gate/up GEMV + SwiGLU)"
+                               if fused else "k_int4_rows (top-k + gate/up GEMV + SwiGLU)",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
