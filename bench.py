@@ -11,6 +11,11 @@ Every step uses a different token and the steps rotate over `--layers` independe
 >= layers * 234 MB earlier and are not served from the 256 MB last-level cache: the timed
 bytes come from HBM, as in a real decode that walks through 61 layers.
 
+Before the W counted warm-up steps, the bench runs steps for `--settle-ms` (200 ms) of wall
+time: the GPU comes to the benchmark idle and needs ~0.1 s of load to leave its low clock
+state (with 5 warm-up steps alone, the first timed steps ran ~3 us per layer slower). The line
+reports how many settle steps ran, and per-step median / p90 / max from a separate pass.
+
 Prints ONE JSON line (rank 0). `value` = microseconds per layer (lower is better).
 """
 from __future__ import annotations
@@ -110,6 +115,37 @@ def median_time(fn, budget_s: float, min_reps: int = 3, max_reps: int = 200):
     return statistics.median(times), len(times)
 
 
+def settle(step, ms: float, sync) -> int:
+    """Run `step` back to back for about `ms` milliseconds of wall time before the counted
+    warm-up: a GPU that has been idle (the bench's setup ends in host work) starts at low
+    clocks and needs ~0.1 s of load to reach its steady state; a decode loop runs
+    continuously. Returns the number of steps run."""
+    n, t_end = 0, time.perf_counter() + ms / 1e3
+    while time.perf_counter() < t_end:
+        for _ in range(50):
+            step(n)
+            n += 1
+        sync()
+    return n
+
+
+def per_step_stats(step, first: int, k: int, stream) -> dict:
+    """Median / p90 / max of single steps, each bracketed by its own pair of HIP events on the
+    launch stream (a separate pass after the timed region; the events add a little time)."""
+    from vib3_amd import _hip
+    k = max(1, min(k, 500))
+    ev = [(_hip.Event(), _hip.Event()) for _ in range(k)]
+    for i, (a, b) in enumerate(ev):
+        a.record(stream)
+        step(first + i)
+        b.record(stream)
+    ev[-1][1].synchronize()
+    us = sorted(a.elapsed_ms(b) * 1e3 for a, b in ev)
+    return {"median": round(statistics.median(us), 3),
+            "p90": round(us[min(len(us) - 1, int(0.9 * len(us)))], 3),
+            "max": round(us[-1], 3), "steps": k}
+
+
 def cpu_baseline(cfg, bank, w, b, x, ids, wts, budget_s: float):
     """Time the oracle (C restatement of vib3's CPU fallback) on the same layer and token, with
     every thread of the process's CPU share and with one thread."""
@@ -178,6 +214,7 @@ def bench_c4(args, cfg) -> int:
         if rc:
             raise _lib.Vib3Error("vib3_launch_moe_mxfp4_batched", rc)
 
+    n_settle = settle(step, args.settle_ms, torch.cuda.synchronize)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -188,6 +225,7 @@ def bench_c4(args, cfg) -> int:
     e1.record(st)
     e1.synchronize()
     us = e0.elapsed_ms(e1) * 1e3 / args.steps
+    step_stats = per_step_stats(step, args.warmup + args.steps, args.steps, st)
 
     # algorithmic bytes: every touched expert's three pages once, activations in, output out
     ebytes = banks[0].expert_bytes
@@ -249,6 +287,8 @@ def bench_c4(args, cfg) -> int:
         "mfma": {"achieved_tflops": round(flops / (us * 1e-6) / 1e12, 2), "peak_tflops_bf16": 2500.0,
                  "frac": round(flops / (us * 1e-6) / 2.5e15, 5)},
         "tokens_per_s": round(T / (us * 1e-6)),
+        "per_step_us": step_stats,
+        "settle": {"ms": args.settle_ms, "steps": n_settle},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -313,6 +353,7 @@ def bench_fp4(args, cfg) -> int:
         if rc:
             raise _lib.Vib3Error("fp4 fused step", rc)
 
+    n_settle = settle(step, args.settle_ms, torch.cuda.synchronize)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -323,6 +364,7 @@ def bench_fp4(args, cfg) -> int:
     e1.record(st)
     e1.synchronize()
     us = e0.elapsed_ms(e1) * 1e3 / args.steps
+    step_stats = per_step_stats(step, args.warmup + args.steps, args.steps, st)
     nbytes = K * ebytes + H * 4 + H // 2 + H // 32 + 2 * H * 4
     gbs = nbytes / (us * 1e-6) / 1e9
     log(f"[bench] fp4 fused: {us:.2f} us/layer, {gbs:.0f} GB/s")
@@ -345,6 +387,8 @@ def bench_fp4(args, cfg) -> int:
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": "profiles/traffic_fp4.json" if traffic else None},
         "cpu_baseline": None,
+        "per_step_us": step_stats,
+        "settle": {"ms": args.settle_ms, "steps": n_settle},
     }
     print(json.dumps(out_line), flush=True)
     return 0
@@ -360,6 +404,9 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--settle-ms", type=float, default=200.0,
+                    help="untimed steps before the warm-up, until the GPU clocks settle "
+                         "(0: none; the number is reported)")
     ap.add_argument("--sublayer", action="store_true",
                     help="the whole MoE sublayer as the engine runs it: x is the f32 residual "
                          "stream, RMSNorm + shared-expert sigmoid gate + residual add fused in")
@@ -444,6 +491,7 @@ def main() -> int:
         if rc:
             raise _lib.Vib3Error("vib3_launch_moe_int4_layer", rc)
 
+    n_settle = settle(lambda i: step(i), args.settle_ms, torch.cuda.synchronize)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -457,7 +505,8 @@ def main() -> int:
     torch.cuda.synchronize()
     total_ms = e0.elapsed_ms(e1)
     us_per_layer = total_ms * 1e3 / args.steps
-    log(f"[bench] {args.steps} steps: {us_per_layer:.2f} us/layer")
+    log(f"[bench] {args.steps} steps: {us_per_layer:.2f} us/layer (after {n_settle} settle steps)")
+    step_stats = per_step_stats(step, args.warmup + args.steps, args.steps, st)
 
     # per-stage times: each stage's launches alone, back to back over the same rotation of
     # layers and tokens (a stage reads what the full-layer launches above left in its workspace)
@@ -554,6 +603,8 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": nbytes["gateup"],
                      "avg_launch_us": round(stage_us["gateup"], 3)},
         "stages_us": {k: round(v, 3) for k, v in stage_us.items()},
+        "per_step_us": step_stats,
+        "settle": {"ms": args.settle_ms, "steps": n_settle},
         "layer_gbs": round(layer_gbs, 1),
         "expert_gemv_gbs": round(expert_gbs, 1),
         "copy_gbs": round(copy_gbs, 1) if copy_gbs else None,

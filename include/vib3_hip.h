@@ -96,6 +96,12 @@ int vib3_launch_weighted_accumulate_f32_dev_scalar(void *output, const void *exp
                                                    const void *dev_weight, int dim,
                                                    void *stream);
 
+/* cuda_ffi.rs:267 (kernels.cu:829, :1143): scores[e] = sum_d h_f16[d] * W_f16[e][d] in f32,
+ * the GEMV of the reference's GPU router branch (gpu_run_router, kernels.rs:2445-2465); the
+ * host does the top-k on the copied scores. One workgroup per expert row (any D, any E). */
+int vib3_launch_router_gemv(const void *hidden_state, const void *router_weights, float *scores,
+                            int hidden_dim, int num_experts, void *stream);
+
 /* cuda_ffi.rs:369 (kernels.cu:665, :1477): scores[e] = sum_d h_f32[d] * W_f16[e][d]. */
 int vib3_launch_router_gemv_f32(const void *hidden_state, const void *router_weights,
                                 float *scores, int hidden_dim, int num_experts, void *stream);

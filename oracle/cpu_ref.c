@@ -882,3 +882,138 @@ void v3o_fp4_to_tiled(const uint8_t *src, uint8_t *dst, size_t m, size_t k)
         for (size_t t = 0; t < nkt; t++)
             memcpy(dst + ((row / 16) * nkt + t) * 512 + (row % 16) * 32, src + row * pk + t * 32, 32);
 }
+
+/* ------------------------------------------------------------------ NVFP4 weight quantizers */
+
+/* Nearest E2M1 magnitude index of a non-negative value by the midpoint ladder of
+ * kernels.rs:3952-3970 / :4052-4072 (a value on a midpoint goes to the larger magnitude;
+ * NaN compares false everywhere and lands on 7). */
+static uint8_t nvfp4_nearest(float v)
+{
+    static const float mid[7] = {0.25f, 0.75f, 1.25f, 1.75f, 2.5f, 3.5f, 5.0f};
+    for (uint8_t i = 0; i < 7; i++)
+        if (v < mid[i]) return i;
+    return 7;
+}
+
+/* One row of kernels.rs:4085-4170 (quantize_weights_to_nvfp4) and of the second half of
+ * :3998-4040 (convert_int4_to_nvfp4): per block of 32 columns, scale = max|w| / 6 in f32
+ * (1.0 for an all-zero block), stored as f16; nibble = nearest(min(|w| / scale, 6)) with the
+ * sign in bit 3 for w < 0; even column in the low nibble. Rust's f32::max / f32::min ignore a
+ * NaN operand, as fmaxf / fminf do. */
+static void nvfp4_quant_row(const float *row, size_t cols, uint8_t *data, uint8_t *scales)
+{
+    const size_t nb = (cols + 31) / 32;
+    for (size_t b = 0; b < nb; b++) {
+        const size_t c0 = b * 32, c1 = c0 + 32 < cols ? c0 + 32 : cols;
+        float amax = 0.0f;
+        for (size_t c = c0; c < c1; c++) amax = fmaxf(amax, fabsf(row[c]));
+        const float scale = amax > 0.0f ? amax / 6.0f : 1.0f;
+        const uint16_t sb = v3o_f32_to_f16(scale);
+        scales[2 * b] = (uint8_t)(sb & 0xff);
+        scales[2 * b + 1] = (uint8_t)(sb >> 8);
+        for (size_t c = c0; c < c1; c++) {
+            const float v = row[c];
+            const uint8_t sign = v < 0.0f ? 1 : 0;
+            const uint8_t nib = (uint8_t)(nvfp4_nearest(fminf(fabsf(v) / scale, 6.0f)) | (sign << 3));
+            data[c / 2] |= (uint8_t)((c % 2 == 0) ? (nib & 0x0f) : ((nib & 0x0f) << 4));
+        }
+    }
+}
+
+size_t v3o_nvfp4_page_bytes(size_t rows, size_t cols)
+{
+    return rows * ((cols + 1) / 2) + rows * ((cols + 31) / 32) * 2;
+}
+
+void v3o_quantize_weights_to_nvfp4(const float *w, size_t rows, size_t cols, uint8_t *out)
+{
+    const size_t pk = (cols + 1) / 2, nb = (cols + 31) / 32;
+    memset(out, 0, v3o_nvfp4_page_bytes(rows, cols));
+    for (size_t r = 0; r < rows; r++)
+        nvfp4_quant_row(w + r * cols, cols, out + r * pk, out + rows * pk + r * nb * 2);
+}
+
+/* kernels.rs:4172-4188: f16 / bf16 weights widened to f32, then the quantizer above. */
+void v3o_quantize_half_to_nvfp4(const uint16_t *w, int dt, size_t rows, size_t cols,
+                                uint8_t *out)
+{
+    float *f = (float *)malloc(rows * cols * sizeof(float));
+    if (!f) return;
+    v3o_to_f32(w, dt, rows * cols, f);
+    v3o_quantize_weights_to_nvfp4(f, rows, cols, out);
+    free(f);
+}
+
+/* kernels.rs:3937-4060 convert_int4_to_nvfp4: each INT4 row dequantized with its BF16 group
+ * scales (w = (q - 8) * s; a scale whose two bytes lie past `len` reads as 1.0, the
+ * reference's bounds rule), then quantized to NVFP4 as above. `len` is the INT4 buffer's
+ * byte length. */
+void v3o_convert_int4_to_nvfp4(const uint8_t *int4, size_t len, size_t rows, size_t cols,
+                               size_t g, uint8_t *out)
+{
+    const size_t pk = (cols + 1) / 2, ng = (cols + g - 1) / g, nb = (cols + 31) / 32;
+    const size_t tot = rows * pk;
+    float *row = (float *)malloc(cols * sizeof(float));
+    if (!row) return;
+    memset(out, 0, v3o_nvfp4_page_bytes(rows, cols));
+    for (size_t r = 0; r < rows; r++) {
+        for (size_t j = 0; j < pk; j++) {
+            const uint8_t b = int4[r * pk + j];
+            const size_t c0 = 2 * j, c1 = c0 + 1;
+            const size_t o0 = tot + (r * ng + c0 / g) * 2;
+            const float s0 = o0 + 1 < len ? v3o_bf16_to_f32((uint16_t)(int4[o0] | (int4[o0 + 1] << 8)))
+                                          : 1.0f;
+            row[c0] = ((float)(b & 0x0f) - 8.0f) * s0;
+            if (c1 < cols) {
+                const size_t o1 = tot + (r * ng + c1 / g) * 2;
+                const float s1 = o1 + 1 < len
+                                     ? v3o_bf16_to_f32((uint16_t)(int4[o1] | (int4[o1 + 1] << 8)))
+                                     : 1.0f;
+                row[c1] = ((float)((b >> 4) & 0x0f) - 8.0f) * s1;
+            }
+        }
+        nvfp4_quant_row(row, cols, out + r * pk, out + rows * pk + r * nb * 2);
+    }
+    free(row);
+}
+
+/* kernels.cu:6017-6128 vib3_fp16_to_nvfp4_weight_kernel: each row's 32-value groups quantized
+ * like the activation (E8M0 of the group's absolute maximum, codes E2M1 round-to-nearest-even
+ * of v * 2^(127-e), split-half within the group), the scale stored as the bf16 e << 7. This
+ * follows the kernel's sm_120 branch (__nv_fp4x4_e2m1, cvt.rn.satfinite); its software branch
+ * for older GPUs uses the midpoint ladder instead, which differs only on exact ties. */
+void v3o_fp16_to_nvfp4_weight(const uint16_t *w_f16, size_t m, size_t k, uint8_t *data,
+                              uint16_t *scales)
+{
+    const size_t G = k / 32;
+    float *row = (float *)malloc(k * sizeof(float));
+    uint8_t *e = (uint8_t *)malloc(G + 1);
+    if (!row || !e) { free(row); free(e); return; }
+    for (size_t r = 0; r < m; r++) {
+        v3o_to_f32(w_f16 + r * k, V3O_F16, k, row);
+        v3o_fp4_quantize_act(row, G * 32, data + r * (k / 2), e);
+        for (size_t g = 0; g < G; g++) scales[r * G + g] = (uint16_t)(e[g] << 7);
+    }
+    free(row);
+    free(e);
+}
+
+/* Row-major sequential NVFP4 (two codes per byte, low nibble = even column) with full BF16
+ * block scales: out[r] = sum_k x[k] * e2m1(q) * bf16(s) in f64 (the reference's scalar GPU
+ * kernels, kernels.cu:446-505, :1957-2090, accumulate per thread and reduce per warp, an
+ * order this restatement does not fix; tests compare within a tolerance). */
+void v3o_nvfp4_seq_matvec_f64(const float *x, const uint8_t *data, const uint16_t *scales,
+                              size_t m, size_t k, double *out)
+{
+    const size_t pk = (k + 1) / 2, nb = (k + 31) / 32;
+    for (size_t r = 0; r < m; r++) {
+        double acc = 0.0;
+        for (size_t c = 0; c < k; c++) {
+            const uint8_t b = data[r * pk + c / 2];
+            const uint8_t q = (c % 2 == 0) ? (b & 0x0f) : (b >> 4);
+            acc += (double)x[c] * (double)v3o_e2m1(q) * (double)v3o_bf16_to_f32(scales[r * nb + c / 32]);
+        }
+        out[r] = acc;
+    }
+}

@@ -28,6 +28,10 @@
  *   v3o_nvfp4_matvec         <- cuda/src/kernels.cu:5357-5449 (tiled split-half MMA GEMV)
  *   v3o_moe_experts_fused    <- cuda/src/kernels.cu:5650-5834, :5868-5990 (fused NVFP4 MoE)
  *   v3o_fp4_split_half / v3o_fp4_to_tiled <- cuda/src/kernels.cu:4132-4160, :4190-4225
+ *   v3o_quantize_weights_to_nvfp4 <- src/compute/kernels.rs:4085-4170
+ *   v3o_quantize_half_to_nvfp4    <- src/compute/kernels.rs:4172-4188
+ *   v3o_convert_int4_to_nvfp4     <- src/compute/kernels.rs:3937-4060
+ *   v3o_fp16_to_nvfp4_weight      <- cuda/src/kernels.cu:6017-6128
  *   v3o_synth_*              synthetic-data generator spec shared with vib3_amd/csrc/synth.hip
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library,
@@ -173,6 +177,26 @@ void v3o_moe_experts_fused(const uint8_t *act_codes, const uint8_t *act_scales,
                            size_t m_out, float *out);
 void v3o_fp4_split_half(uint8_t *data, size_t nbytes);
 void v3o_fp4_to_tiled(const uint8_t *src, uint8_t *dst, size_t m, size_t k);
+
+/* ---- NVFP4 weight quantizers (row-major sequential E2M1, FP16 block scales per 32) ---- */
+size_t v3o_nvfp4_page_bytes(size_t rows, size_t cols);
+/* kernels.rs:4085 quantize_weights_to_nvfp4: out = [rows x ceil(cols/2)] codes then
+ * [rows x ceil(cols/32)] f16 scales (max|w| / 6) */
+void v3o_quantize_weights_to_nvfp4(const float *w, size_t rows, size_t cols, uint8_t *out);
+/* kernels.rs:4172 / :4183 quantize_{fp16,bf16}_to_nvfp4 (dt = V3O_F16 / V3O_BF16) */
+void v3o_quantize_half_to_nvfp4(const uint16_t *w, int dt, size_t rows, size_t cols,
+                                uint8_t *out);
+/* kernels.rs:3937 convert_int4_to_nvfp4 (INT4 page with BF16 group scales of size g; len =
+ * the page's byte length, for the reference's bounds rule) */
+void v3o_convert_int4_to_nvfp4(const uint8_t *int4, size_t len, size_t rows, size_t cols,
+                               size_t g, uint8_t *out);
+/* kernels.cu:6017 vib3_fp16_to_nvfp4_weight: f16 [m][k] -> row-major split-half E2M1 codes
+ * [m][k/2] and bf16 scales 2^(e-127) ([m][k/32], E8M0 e in bits 7..14), k a multiple of 32 */
+void v3o_fp16_to_nvfp4_weight(const uint16_t *w_f16, size_t m, size_t k, uint8_t *data,
+                              uint16_t *scales);
+/* f64 matvec of a row-major sequential NVFP4 matrix with full BF16 scales */
+void v3o_nvfp4_seq_matvec_f64(const float *x, const uint8_t *data, const uint16_t *scales,
+                              size_t m, size_t k, double *out);
 
 /* ---- synthetic data generator (counter-based, identical spec in csrc/synth.hip) ---- */
 uint64_t v3o_synth_hash(uint64_t seed, uint64_t stream, uint64_t ctr);

@@ -80,6 +80,12 @@ def _declare(L: C.CDLL) -> None:
         "v3o_moe_mxfp4_batched": (None, [P, S, S, S, P, S, P, P, S, P, I]),
         "v3o_synth_e8m0": (C.c_uint8, [U64, U64, U64]),
         "v3o_synth_mxfp4_page": (None, [U64, U64, S, S, S, P]),
+        "v3o_nvfp4_page_bytes": (S, [S, S]),
+        "v3o_quantize_weights_to_nvfp4": (None, [P, S, S, P]),
+        "v3o_quantize_half_to_nvfp4": (None, [P, I, S, S, P]),
+        "v3o_convert_int4_to_nvfp4": (None, [P, S, S, S, S, P]),
+        "v3o_fp16_to_nvfp4_weight": (None, [P, S, S, P, P]),
+        "v3o_nvfp4_seq_matvec_f64": (None, [P, P, P, S, S, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -431,3 +437,49 @@ def fp4_to_tiled(src, m, k) -> np.ndarray:
     dst = np.zeros(m * k // 2, dtype=np.uint8)
     lib().v3o_fp4_to_tiled(_p(s), _p(dst), m, k)
     return dst
+
+
+# ---------------------------------------------------------------- NVFP4 weight quantizers
+
+def quantize_weights_to_nvfp4(w, rows, cols) -> np.ndarray:
+    """kernels.rs:4085: row-major E2M1 codes (low nibble = even column), then f16 scales."""
+    w = np.ascontiguousarray(w, dtype=np.float32).ravel()
+    assert w.size == rows * cols
+    out = np.zeros(lib().v3o_nvfp4_page_bytes(rows, cols), dtype=np.uint8)
+    lib().v3o_quantize_weights_to_nvfp4(_p(w), rows, cols, _p(out))
+    return out
+
+
+def quantize_half_to_nvfp4(bits, dt, rows, cols) -> np.ndarray:
+    """kernels.rs:4172 (dt F16) / :4183 (dt BF16)."""
+    b = np.ascontiguousarray(bits, dtype=np.uint16).ravel()
+    out = np.zeros(lib().v3o_nvfp4_page_bytes(rows, cols), dtype=np.uint8)
+    lib().v3o_quantize_half_to_nvfp4(_p(b), dt, rows, cols, _p(out))
+    return out
+
+
+def convert_int4_to_nvfp4(page, rows, cols, g) -> np.ndarray:
+    """kernels.rs:3937: INT4 page (BF16 group scales) -> NVFP4 page (f16 block scales)."""
+    p = np.ascontiguousarray(page, dtype=np.uint8).ravel()
+    out = np.zeros(lib().v3o_nvfp4_page_bytes(rows, cols), dtype=np.uint8)
+    lib().v3o_convert_int4_to_nvfp4(_p(p), p.size, rows, cols, g, _p(out))
+    return out
+
+
+def fp16_to_nvfp4_weight(w_f16_bits, m, k):
+    """kernels.cu:6017: (row-major split-half codes [m*k/2], bf16 E8M0 scales [m*k/32])."""
+    b = np.ascontiguousarray(w_f16_bits, dtype=np.uint16).ravel()
+    data = np.zeros(m * k // 2, dtype=np.uint8)
+    sc = np.zeros(m * (k // 32), dtype=np.uint16)
+    lib().v3o_fp16_to_nvfp4_weight(_p(b), m, k, _p(data), _p(sc))
+    return data, sc
+
+
+def nvfp4_seq_matvec_f64(x, data, scales, m, k) -> np.ndarray:
+    """f64 matvec of a row-major sequential NVFP4 matrix with full bf16 scales."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    s = np.ascontiguousarray(scales, dtype=np.uint16)
+    out = np.empty(m, dtype=np.float64)
+    lib().v3o_nvfp4_seq_matvec_f64(_p(x), _p(d), _p(s), m, k, _p(out))
+    return out

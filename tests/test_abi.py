@@ -22,7 +22,7 @@ def test_header_declares_the_reference_launchers():
     for ref_name in ["vib3_launch_partial_matmul_int4", "vib3_launch_partial_matmul_int4_f32",
                      "vib3_launch_fused_swiglu_int4_f32", "vib3_launch_silu_mul",
                      "vib3_launch_weighted_accumulate_f32",
-                     "vib3_launch_weighted_accumulate_f32_f32", "vib3_launch_router_gemv_f32",
+                     "vib3_launch_weighted_accumulate_f32_f32", "vib3_launch_router_gemv_f32", "vib3_launch_router_gemv",
                      "vib3_launch_router_topk", "vib3_launch_rms_norm_f32",
                      "vib3_launch_rms_norm_f32_to_f16", "vib3_launch_residual_add_f32_f32",
                      "vib3_launch_sigmoid_gated_accumulate_f32"]:

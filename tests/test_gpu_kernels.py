@@ -334,6 +334,31 @@ def test_legacy_router_topk_and_gemv():
     assert float(wts.sum().item()) == pytest.approx(2.5, rel=1e-5)
 
 
+@pytest.mark.parametrize("E,D", [(8, 4096), (384, 7168)])
+def test_router_gemv_f16(E, D):
+    """vib3_launch_router_gemv (cuda_ffi.rs:267, kernels.cu:829): f16 h x f16 W -> f32 scores,
+    the GEMV of the reference's GPU router branch (kernels.rs:2465); the host then selects."""
+    L = _lib()
+    _say(f"case: router_gemv E={E} D={D}")
+    w = O.synth_normal_array(11, 3, 0, E * D, 0.02, O.F16)
+    xt, xh = act(D, O.F16)
+    dw = _dev(w)
+    scores = torch.full((E,), float("nan"), dtype=torch.float32, device="cuda")
+    L.call("vib3_launch_router_gemv", xt.data_ptr(), dw.data_ptr(), scores.data_ptr(), D, E,
+           _stream())
+    torch.cuda.synchronize()
+    _, _, r_scores = O.router(xh, w, O.F16, E, D, 2, 0, 1.0, True, None)
+    got = scores.cpu().numpy()
+    # f32 sums in another order: |err| <= D * eps * sum|x*w|, far below 1e-5 relative L2
+    assert np.isfinite(got).all()
+    assert rel_l2(got, r_scores) <= 1e-5
+    # the selection the host makes from them (softmax top-2) matches the oracle's
+    k = 2
+    if topk_margin_ok(r_scores, k):
+        assert np.argsort(-got, kind="stable")[:k].tolist() == \
+            np.argsort(-r_scores, kind="stable")[:k].tolist()
+
+
 def test_router_ties_are_stable():
     L = _lib()
     _say("case: router ties")

@@ -82,6 +82,7 @@ SIGNATURES = {
     "vib3_launch_weighted_accumulate_f32_f32": (I, [P, P, F, I, P]),
     "vib3_launch_weighted_accumulate": (I, [P, P, F, I, P]),
     "vib3_launch_weighted_accumulate_f32_dev_scalar": (I, [P, P, P, I, P]),
+    "vib3_launch_router_gemv": (I, [P, P, P, I, I, P]),
     "vib3_launch_router_gemv_f32": (I, [P, P, P, I, I, P]),
     "vib3_launch_router_topk": (I, [P, P, P, P, P, P, I, I, I, I, F, P]),
     "vib3_launch_rms_norm_f32": (I, [P, P, P, I, F, P]),
@@ -138,7 +139,10 @@ def load() -> C.CDLL:
                 f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`"
                 " or `python vib3_amd/build.py`")
         lib = C.CDLL(LIB_PATH)
+        alt = bool(os.environ.get("VIB3_LIB"))  # another build may predate some entry points
         for name, (res, args) in SIGNATURES.items():
+            if alt and not hasattr(lib, name):
+                continue
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args

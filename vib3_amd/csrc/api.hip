@@ -266,6 +266,16 @@ int vib3_launch_weighted_accumulate_f32_f32(void* output, const void* expert_out
   VIB3_RETURN_LAUNCH();
 }
 
+int vib3_launch_router_gemv(const void* hidden_state, const void* router_weights, float* scores,
+                            int hidden_dim, int num_experts, void* stream) {
+  if (hidden_dim <= 0 || num_experts <= 0) return VIB3_ERR_BAD_COUNT;
+  if (!hidden_state || !router_weights || !scores) return VIB3_ERR_BAD_POINTER;
+  RouterArgs a{};
+  a.x = hidden_state; a.x_dt = VIB3_DT_F16; a.w = router_weights; a.w_dt = VIB3_DT_F16;
+  a.D = hidden_dim; a.E = num_experts; a.scores = scores;
+  return launch_router_logits(a, S(stream));
+}
+
 int vib3_launch_router_gemv_f32(const void* hidden_state, const void* router_weights,
                                 float* scores, int hidden_dim, int num_experts, void* stream) {
   if (hidden_dim <= 0 || num_experts <= 0) return VIB3_ERR_BAD_COUNT;

@@ -230,6 +230,19 @@ def run_router_with_scoring_and_bias(hidden_state: torch.Tensor, router_weights:
     return list(zip(ids_h, wts.cpu().tolist()))
 
 
+def router_gemv(hidden_state: torch.Tensor, router_weights: torch.Tensor, scores: torch.Tensor,
+                hidden_dim: int, num_experts: int) -> None:
+    """cuda_ffi.rs:267 vib3_launch_router_gemv: f16 h x f16 W -> f32 scores on the device, the
+    GEMV step of gpu_run_router (kernels.rs:2445-2465)."""
+    if hidden_state.dtype != torch.float16 or router_weights.dtype != torch.float16:
+        raise TypeError("router_gemv takes f16 hidden_state and f16 router_weights")
+    if scores.dtype != torch.float32 or scores.numel() < num_experts:
+        raise ValueError("scores must be f32 with at least num_experts elements")
+    _lib.call("vib3_launch_router_gemv", _dev(hidden_state, "hidden_state"),
+              _dev(router_weights, "router_weights"), _dev(scores, "scores"), hidden_dim,
+              num_experts, _stream(hidden_state))
+
+
 def run_router_gpu_topk(hidden_state, router_weights, num_experts, hidden_dim, top_k,
                         scoring_func, scores_dev=None, topk_ids_dev=None, topk_weights_dev=None):
     """kernels.rs:1811 run_router_gpu_topk (bias always NULL there)."""
