@@ -180,6 +180,9 @@ int vib3_launch_router_topk_ex(const void *hidden, int hidden_dtype, const void 
  * gives up after 64 polls, so vib3_moe_int4_layer_status reports 1. Every kernel still exits
  * normally; the routing of such a launch is meaningless. */
 #define VIB3_MOE_TEST_ROUTER_TIMEOUT 0x100
+/* RMSNorm and shared-expert gates in a prologue kernel of their own instead of inside the
+ * gate/up kernel (same results bit for bit; for tests and timing). */
+#define VIB3_MOE_SEPARATE_PROLOGUE 0x200
 
 typedef struct vib3_moe_int4_layer {
     /* activation: x[hidden] */
@@ -296,9 +299,17 @@ int vib3_launch_quantize_activation_fp4_fast(const void *input, void *act_fp4,
                                              void *act_scales, int K, void *stream);
 
 /* cuda_ffi.rs:1026 (kernels.cu:6507): allocate the fused MoE's intermediate buffer (FP4 h of 8
- * experts) on the current device; call once before launches and before graph capture. The
- * fused launches never allocate: without it they return VIB3_ERR_WORKSPACE. */
+ * experts) on the current device. Without it, the first launch of the entry points below
+ * that take no workspace allocates it (the reference's ensure_moe_bufs, kernels.cu:5675);
+ * call it before graph capture, where a launch that would allocate returns
+ * VIB3_ERR_WORKSPACE instead. Those entry points share this one buffer per device: launches
+ * on one device must be ordered (one stream at a time); for concurrent streams use the _ws
+ * forms, each with a workspace of its own. */
 int vib3_moe_prewarm_gpu_bufs(int m_mid, int k_mid);
+
+/* Bytes of the caller workspace of the _ws forms below (256-byte aligned device memory). No
+ * reference counterpart. */
+size_t vib3_moe_experts_fused_workspace_bytes(int m_mid);
 
 /* cuda_ffi.rs:809 (kernels.cu:5650): host arrays of device pointers per expert (data and
  * scales of up, gate, down) and host routing weights; layer_output accumulated (+=). */
@@ -321,6 +332,109 @@ int vib3_launch_moe_experts_fused_gpu(const void *act_fp4, const void *act_scale
                                       const float *expert_weights, int layer,
                                       int num_experts_total, int num_active, int K_in, int M_mid,
                                       int K_mid, int M_out, float *layer_output, void *stream);
+
+/* vib3_launch_moe_experts_fused[_gpu] with the intermediate buffer in the caller's workspace
+ * (vib3_moe_experts_fused_workspace_bytes(M_mid) bytes, 256-byte aligned): reentrant, so
+ * launches on different streams with different workspaces may overlap. No reference
+ * counterpart (additive). */
+int vib3_launch_moe_experts_fused_ws(const void *act_fp4, const void *act_scales,
+                                     const void *const *up_weight_ptrs,
+                                     const void *const *up_scale_ptrs,
+                                     const void *const *gate_weight_ptrs,
+                                     const void *const *gate_scale_ptrs,
+                                     const void *const *down_weight_ptrs,
+                                     const void *const *down_scale_ptrs,
+                                     const float *expert_weights_host, int num_experts, int K_in,
+                                     int M_mid, int K_mid, int M_out, float *layer_output,
+                                     void *workspace, size_t workspace_bytes, void *stream);
+int vib3_launch_moe_experts_fused_gpu_ws(const void *act_fp4, const void *act_scales,
+                                         const uint64_t *page_table, const uint16_t *expert_ids,
+                                         const float *expert_weights, int layer,
+                                         int num_experts_total, int num_active, int K_in,
+                                         int M_mid, int K_mid, int M_out, float *layer_output,
+                                         void *workspace, size_t workspace_bytes, void *stream);
+
+/* cuda_ffi.rs:671 (kernels.cu:4708): one expert over tiled split-half pages: up and gate
+ * GEMVs, SwiGLU, FP4 h, down GEMV, layer_output += expert_weight * down (the fused pipeline
+ * above with one expert; same buffer rule). */
+int vib3_launch_expert_batched(const void *act_fp4, const void *act_scales,
+                               const void *up_weight, const void *up_scales,
+                               const void *gate_weight, const void *gate_scales,
+                               const void *down_weight, const void *down_scales,
+                               float *layer_output, float expert_weight, int K_in, int M_mid,
+                               int K_mid, int M_out, void *stream);
+
+/* cuda_ffi.rs:851 (kernels.cu:6017-6154): f16 weights [M][K] -> row-major split-half E2M1
+ * codes [M][K/2] and bf16 scales [M][K/32] = 2^(e - 127) with e the E8M0 of each 32-value
+ * group (the activation quantizer's rule). K % 32 == 0. */
+int vib3_launch_fp16_to_nvfp4_weight(const void *input, void *out_data, void *out_scales, int M,
+                                     int K, void *stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Per-page NVFP4 GEMVs (fp4_pages.hip), the reference's launchers for NVFP4 experts spread
+ * over several pages (engine.rs:5960-6226). A page is [M][K/2] code bytes then [M][K/32]
+ * 2-byte scales. K % 32 == 0 (tiled: K % 64 == 0, M % 16 == 0), data 16-byte aligned.
+ * Block-scaled (E2M1 x FP4 activation): exact group sums in f64, one rounding to f32 output;
+ * the scale's exponent byte is the E8M0 (gemv_scalar: its bf16 value).
+ * ---------------------------------------------------------------------------------------- */
+
+/* cuda_ffi.rs:634 (kernels.cu:3752): row-major split-half weights, pre-quantized activation. */
+int vib3_launch_gemv_mma_nvfp4_preq(const void *act_fp4, const void *act_scales,
+                                    const void *weight_packed, const void *scales, void *output,
+                                    int K, int M_slice, void *stream);
+/* cuda_ffi.rs:690 (kernels.cu:5229): the same. */
+int vib3_launch_gemv_mma_nvfp4_preq_fast(const void *act_fp4, const void *act_scales,
+                                         const void *weight_packed, const void *scales,
+                                         void *output, int K, int M_slice, void *stream);
+/* cuda_ffi.rs:646 (kernels.cu:3853, :3789): output = (g * sigmoid(g)) * u of the up and gate
+ * GEMVs above, f32. */
+int vib3_launch_fused_swiglu_mma_nvfp4_preq(const void *act_fp4, const void *act_scales,
+                                            const void *up_weight, const void *up_scales,
+                                            const void *gate_weight, const void *gate_scales,
+                                            void *output, int K, int M_slice, void *stream);
+/* cuda_ffi.rs:793 (kernels.cu:5267): the same. */
+int vib3_launch_fused_swiglu_mma_nvfp4_preq_fast(const void *act_fp4, const void *act_scales,
+                                                 const void *up_weight, const void *up_scales,
+                                                 const void *gate_weight, const void *gate_scales,
+                                                 void *output, int K, int M_slice, void *stream);
+/* cuda_ffi.rs:729 (kernels.cu:4359): tiled split-half weights. */
+int vib3_launch_gemv_mma_nvfp4_tiled(const void *act_fp4, const void *act_scales,
+                                     const void *weight, const void *scales, void *output, int K,
+                                     int M_slice, void *stream);
+/* cuda_ffi.rs:703 (kernels.cu:4520): row-major split-half weights, scales read as bf16 values. */
+int vib3_launch_gemv_scalar_nvfp4(const void *act_fp4, const void *act_scales,
+                                  const void *weight_packed, const void *scales, void *output,
+                                  int K, int M_slice, void *stream);
+/* cuda_ffi.rs:599 / :611 (kernels.cu:3676, :3807): f32 input quantized to FP4 in the kernel
+ * (vib3_launch_quantize_activation_fp4's rule), sequential-nibble weights. */
+int vib3_launch_gemv_mma_nvfp4(const void *input, const void *weight_packed, const void *scales,
+                               void *output, int K, int M_slice, void *stream);
+int vib3_launch_fused_swiglu_mma_nvfp4(const void *input, const void *up_weight,
+                                       const void *up_scales, const void *gate_weight,
+                                       const void *gate_scales, void *output, int K,
+                                       int M_slice, void *stream);
+
+/* Scalar NVFP4 GEMVs (cuda_ffi.rs:532-597; kernels.cu:446, :512, :598, :1957, :2035): f32 (or
+ * f16: _fp16in) input times sequential-nibble E2M1 weights times the bf16 block scale
+ * (block_size a power-of-two multiple of 32), accumulated in f32; f16 output (or f32: _f32out);
+ * SwiGLU output silu(g) * u with silu(g) = g / (1 + e^-g). */
+int vib3_launch_partial_matmul_nvfp4(const void *input, const void *weight_packed,
+                                     const void *scales, void *output, int K, int M_slice,
+                                     int block_size, void *stream);
+int vib3_launch_partial_matmul_nvfp4_f32out(const void *input, const void *weight_packed,
+                                            const void *scales, void *output, int K, int M_slice,
+                                            int block_size, void *stream);
+int vib3_launch_partial_matmul_nvfp4_fp16in(const void *input, const void *weight_packed,
+                                            const void *scales, void *output, int K, int M_slice,
+                                            int block_size, void *stream);
+int vib3_launch_fused_swiglu_nvfp4(const void *input, const void *up_weight,
+                                   const void *up_scales, const void *gate_weight,
+                                   const void *gate_scales, void *output, int K, int M_slice,
+                                   int block_size, void *stream);
+int vib3_launch_fused_swiglu_nvfp4_f32out(const void *input, const void *up_weight,
+                                          const void *up_scales, const void *gate_weight,
+                                          const void *gate_scales, void *output, int K,
+                                          int M_slice, int block_size, void *stream);
 
 /* cuda_ffi.rs:662 (kernels.cu:4132-4183): sequential nibble order -> split-half, in place, per
  * 16-byte block of the page's data (a partial last block is left as it is). */

@@ -1017,3 +1017,64 @@ void v3o_nvfp4_seq_matvec_f64(const float *x, const uint8_t *data, const uint16_
         out[r] = acc;
     }
 }
+
+/* ------------------------------------------------------------------ per-page NVFP4 GEMVs */
+
+/* Code of W[row][k] in layout `lay`: 0 = row-major split-half (kernels.cu:3739-3750, after
+ * vib3_launch_repack_weights_inplace), 1 = tiled split-half (kernels.cu:4265), 2 = row-major
+ * sequential (low nibble = even column, the quantizer's layout, kernels.cu:3387). */
+static uint8_t layout_code(const uint8_t *data, size_t row, size_t k, size_t K, int lay)
+{
+    if (lay == 1) return tiled_code(data, row, k, K);
+    const uint8_t *r = data + row * (K / 2);
+    if (lay == 0) return split_code(r, k);
+    const uint8_t b = r[k / 2];
+    return (k % 2 == 0) ? (b & 15) : (b >> 4);
+}
+
+/* The block-scaled GEMV of the reference's per-page MMA kernels (kernels.cu:3276-3385,
+ * :3739-3750, :4265-4358, :4438-4540) with a pre-quantized activation: out[r] = f32(exact
+ * sum over groups g of (sum_j W e2m1 * a e2m1) * s_w(r, g) * 2^(ea_g - 127)), where s_w is
+ * 2^(((s >> 7) & 0xff) - 127) (full = 0: the E8M0 byte the MMA instruction takes) or the bf16
+ * value s (full = 1: vib3_gemv_scalar_nvfp4_kernel, kernels.cu:4480). Exact in f64 for the
+ * scale spreads of real weights; rounded to f32 once. */
+void v3o_nvfp4_page_matvec(const uint8_t *act_codes, const uint8_t *act_scales,
+                           const uint8_t *data, const uint16_t *scales, size_t m, size_t k,
+                           int layout, int full, float *out)
+{
+    const size_t G = k / 32;
+    for (size_t r = 0; r < m; r++) {
+        double acc = 0.0;
+        for (size_t g = 0; g < G; g++) {
+            double s = 0.0;
+            for (size_t j = 0; j < 32; j++) {
+                const size_t kk = g * 32 + j;
+                s += (double)v3o_e2m1(layout_code(data, r, kk, k, layout)) *
+                     (double)v3o_e2m1(split_code(act_codes, kk));
+            }
+            const uint16_t sw = scales[r * G + g];
+            const double ws = full ? (double)v3o_bf16_to_f32(sw) : ldexp(1.0, ((sw >> 7) & 0xff) - 127);
+            acc += s * ws * ldexp(1.0, (int)act_scales[g] - 127);
+        }
+        out[r] = (float)acc;
+    }
+}
+
+/* SwiGLU of two page GEMVs as the reference composes it (kernels.cu:3853-3905 then
+ * vib3_swiglu_fuse_f32_kernel :3789-3800): h = (g * sigmoid(g)) * u, sigmoid = 1 / (1 + e^-g)
+ * with this file's exp (v3o_exp_cw). */
+void v3o_nvfp4_page_swiglu(const uint8_t *act_codes, const uint8_t *act_scales,
+                           const uint8_t *up, const uint16_t *up_s, const uint8_t *gate,
+                           const uint16_t *gate_s, size_t m, size_t k, int layout, float *out)
+{
+    float *u = (float *)malloc(m * sizeof(float)), *g = (float *)malloc(m * sizeof(float));
+    if (!u || !g) { free(u); free(g); return; }
+    v3o_nvfp4_page_matvec(act_codes, act_scales, up, up_s, m, k, layout, 0, u);
+    v3o_nvfp4_page_matvec(act_codes, act_scales, gate, gate_s, m, k, layout, 0, g);
+    for (size_t i = 0; i < m; i++) {
+        const float sig = 1.0f / (1.0f + v3o_exp_cw(-g[i]));
+        out[i] = (g[i] * sig) * u[i];
+    }
+    free(u);
+    free(g);
+}

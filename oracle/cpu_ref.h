@@ -32,6 +32,7 @@
  *   v3o_quantize_half_to_nvfp4    <- src/compute/kernels.rs:4172-4188
  *   v3o_convert_int4_to_nvfp4     <- src/compute/kernels.rs:3937-4060
  *   v3o_fp16_to_nvfp4_weight      <- cuda/src/kernels.cu:6017-6128
+ *   v3o_nvfp4_page_matvec / _swiglu <- cuda/src/kernels.cu:3276-3385, :3739-3905, :4265-4540
  *   v3o_synth_*              synthetic-data generator spec shared with vib3_amd/csrc/synth.hip
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library,
@@ -197,6 +198,16 @@ void v3o_fp16_to_nvfp4_weight(const uint16_t *w_f16, size_t m, size_t k, uint8_t
 /* f64 matvec of a row-major sequential NVFP4 matrix with full BF16 scales */
 void v3o_nvfp4_seq_matvec_f64(const float *x, const uint8_t *data, const uint16_t *scales,
                               size_t m, size_t k, double *out);
+
+/* ---- per-page NVFP4 GEMVs (pre-quantized activation; layout 0 row-major split-half,
+ * 1 tiled, 2 row-major sequential; full = 0: weight scale = E8M0 byte of the bf16, 1: the
+ * bf16 value) ---- */
+void v3o_nvfp4_page_matvec(const uint8_t *act_codes, const uint8_t *act_scales,
+                           const uint8_t *data, const uint16_t *scales, size_t m, size_t k,
+                           int layout, int full, float *out);
+void v3o_nvfp4_page_swiglu(const uint8_t *act_codes, const uint8_t *act_scales,
+                           const uint8_t *up, const uint16_t *up_s, const uint8_t *gate,
+                           const uint16_t *gate_s, size_t m, size_t k, int layout, float *out);
 
 /* ---- synthetic data generator (counter-based, identical spec in csrc/synth.hip) ---- */
 uint64_t v3o_synth_hash(uint64_t seed, uint64_t stream, uint64_t ctr);

@@ -86,6 +86,8 @@ def _declare(L: C.CDLL) -> None:
         "v3o_convert_int4_to_nvfp4": (None, [P, S, S, S, S, P]),
         "v3o_fp16_to_nvfp4_weight": (None, [P, S, S, P, P]),
         "v3o_nvfp4_seq_matvec_f64": (None, [P, P, P, S, S, P]),
+        "v3o_nvfp4_page_matvec": (None, [P, P, P, P, S, S, I, I, P]),
+        "v3o_nvfp4_page_swiglu": (None, [P, P, P, P, P, P, S, S, I, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -482,4 +484,25 @@ def nvfp4_seq_matvec_f64(x, data, scales, m, k) -> np.ndarray:
     s = np.ascontiguousarray(scales, dtype=np.uint16)
     out = np.empty(m, dtype=np.float64)
     lib().v3o_nvfp4_seq_matvec_f64(_p(x), _p(d), _p(s), m, k, _p(out))
+    return out
+
+
+def nvfp4_page_matvec(act_codes, act_scales, data, scales, m, k, layout, full=False):
+    """Block-scaled page GEMV; layout 0 row-major split-half, 1 tiled, 2 sequential."""
+    a = np.ascontiguousarray(act_codes, dtype=np.uint8)
+    s = np.ascontiguousarray(act_scales, dtype=np.uint8)
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    w = np.ascontiguousarray(scales, dtype=np.uint16)
+    out = np.empty(m, dtype=np.float32)
+    lib().v3o_nvfp4_page_matvec(_p(a), _p(s), _p(d), _p(w), m, k, layout, int(full), _p(out))
+    return out
+
+
+def nvfp4_page_swiglu(act_codes, act_scales, up, up_s, gate, gate_s, m, k, layout):
+    a = np.ascontiguousarray(act_codes, dtype=np.uint8)
+    s = np.ascontiguousarray(act_scales, dtype=np.uint8)
+    arrs = [np.ascontiguousarray(v, dtype=t) for v, t in
+            ((up, np.uint8), (up_s, np.uint16), (gate, np.uint8), (gate_s, np.uint16))]
+    out = np.empty(m, dtype=np.float32)
+    lib().v3o_nvfp4_page_swiglu(_p(a), _p(s), *[_p(v) for v in arrs], m, k, layout, _p(out))
     return out

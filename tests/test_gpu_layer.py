@@ -64,8 +64,9 @@ def verify_layer(layer, bank, x, out, router_w_host, w_dt, bias_host, mode, scal
         keys = sig + (bias_host if bias_host is not None else 0)
     else:
         keys = r_scores.astype(np.float64)
-    if not margin_ok(keys, k):
-        pytest.skip("selection margin below 1e-3 for this seed")
+    # the inputs are deterministic: every caller's token clears the bar (a change of seed or
+    # generator that breaks this fails here instead of skipping the parity check)
+    assert margin_ok(keys, k), "selection margin below 1e-3: choose another token"
     assert ids.tolist() == r_ids.tolist()
     assert np.allclose(wts, r_wts, rtol=1e-5)
     routed = {int(e): bank.expert_pages_host(int(e)) for e in r_ids}
@@ -136,8 +137,10 @@ def test_c2_graph_replay(kimi):
 
 def test_router_wait_timeout_reported():
     """A router wait that gives up (forced from the host: the kernels poll for a tag nobody
-    publishes, with a 64-poll limit) is reported by vib3_moe_int4_layer_status; every kernel
-    exits normally and the next ordinary launch is correct."""
+    publishes, with a 64-poll limit) is reported by vib3_moe_int4_layer_status, and the
+    routing is still right: the waiting waves compute the unpublished logits themselves, so
+    the timed-out launch's ids, weights and output equal the oracle's. Every kernel exits
+    normally and the next ordinary launch is correct."""
     from vib3_amd import moe
     from vib3_amd._lib import DT_BF16, MOE_TEST_ROUTER_TIMEOUT, ROUTER_SIGMOID
     _say("case: router wait timeout status")
@@ -150,8 +153,9 @@ def test_router_wait_timeout_reported():
     x = moe.make_activation(shape.hidden, 4, SEED)
     assert layer.status() == 0
     layer.flags = MOE_TEST_ROUTER_TIMEOUT
-    layer.launch(x)
+    out = layer.launch(x).cpu().numpy()
     torch.cuda.synchronize()
+    verify_layer(layer, bank, x, out, w.cpu().numpy(), O.F32, bias.cpu().numpy(), 1, 1.5, 6)
     assert layer.status(clear=True) == 1
     assert layer.status() == 0
     layer.flags = 0

@@ -135,8 +135,7 @@ def test_layer_with_norm_gate_residual(hidden, inter, E, k, ns, layout, use_norm
     r_ids, r_wts, r_scores = O.router(xn, w.cpu().numpy(), O.F32, E, hidden, k, 1, 2.827, True,
                                       bias.cpu().numpy())
     keys = np.sort(1 / (1 + np.exp(-r_scores.astype(np.float64))) + bias.cpu().numpy())[::-1]
-    if keys[k - 1] - keys[k] <= 1e-3:
-        pytest.skip("selection margin below 1e-3 for this seed")
+    assert keys[k - 1] - keys[k] > 1e-3, "selection margin below 1e-3: choose another token"
     assert layer.ids.cpu().numpy().view(np.uint16)[:k].tolist() == r_ids.tolist()
     gates = None
     if use_gate:
@@ -195,12 +194,12 @@ def test_norm_needs_f32_stream():
 
 
 @pytest.mark.parametrize("hidden,inter,E,k,ns", [(1024, 256, 16, 4, 2), (7168, 2048, 384, 8, 1)])
-def test_fused_prologue_equals_prologue_kernel(hidden, inter, E, k, ns, monkeypatch):
+def test_fused_prologue_equals_prologue_kernel(hidden, inter, E, k, ns):
     """The gate/up kernel that normalises x and computes the shared gates itself gives the
     layer of the separate prologue kernel bit for bit (same summation orders), over several
     tokens, with and without the residual."""
     from vib3_amd import moe
-    from vib3_amd._lib import DT_BF16, ROUTER_SIGMOID
+    from vib3_amd._lib import DT_BF16, MOE_SEPARATE_PROLOGUE, ROUTER_SIGMOID
     _say(f"case: fused prologue hidden={hidden} E={E} k={k} shared={ns}")
     sh = _shape(moe, DT_BF16, hidden, inter, E, ns)
     bank = moe.Int4ExpertBank(sh, layer=5, seed=SEED)
@@ -212,13 +211,13 @@ def test_fused_prologue_equals_prologue_kernel(hidden, inter, E, k, ns, monkeypa
     for t in range(3):
         x = torch.from_numpy(_f32(hidden, 20 + t, 20.0)).cuda()
         res = torch.from_numpy(_f32(hidden, 30 + t, 20.0)).cuda() if t != 1 else None
-        monkeypatch.delenv("VIB3_PROLOGUE_KERNEL", raising=False)
+        flags = layer.flags
         fused = layer.launch(x, residual=res).cpu().numpy().copy()
         ids_f = layer.ids.cpu().numpy().copy()
-        monkeypatch.setenv("VIB3_PROLOGUE_KERNEL", "1")
+        layer.flags = flags | MOE_SEPARATE_PROLOGUE
         sep = layer.launch(x, residual=res).cpu().numpy().copy()
         ids_s = layer.ids.cpu().numpy().copy()
-        monkeypatch.delenv("VIB3_PROLOGUE_KERNEL")
+        layer.flags = flags
         assert np.array_equal(ids_f, ids_s)
         assert np.array_equal(fused.view(np.uint32), sep.view(np.uint32)), t
 

@@ -17,6 +17,7 @@ DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 ROUTER_SOFTMAX, ROUTER_SIGMOID = 0, 1
 MOE_F32_INTERMEDIATE = 1
 MOE_TEST_ROUTER_TIMEOUT = 0x100
+MOE_SEPARATE_PROLOGUE = 0x200
 
 ERRORS = {-1: "unsupported shape or dtype", -2: "bad count", -3: "bad pointer or alignment",
           -4: "workspace too small", -5: "unexpected .vib3 file or page layout",
@@ -125,6 +126,24 @@ SIGNATURES = {
     "vib3_launch_repack_weights_inplace": (I, [P, C.c_longlong, P]),
     "vib3_launch_repack_row_to_tiled": (I, [P, P, I, I, P]),
     "vib3_hip_version": (C.c_char_p, []),
+    "vib3_moe_experts_fused_workspace_bytes": (S, [I]),
+    "vib3_launch_moe_experts_fused_ws": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, P, P, S, P]),
+    "vib3_launch_moe_experts_fused_gpu_ws": (I, [P, P, P, P, P, I, I, I, I, I, I, I, P, P, S, P]),
+    "vib3_launch_expert_batched": (I, [P, P, P, P, P, P, P, P, P, F, I, I, I, I, P]),
+    "vib3_launch_fp16_to_nvfp4_weight": (I, [P, P, P, I, I, P]),
+    "vib3_launch_gemv_mma_nvfp4_preq": (I, [P, P, P, P, P, I, I, P]),
+    "vib3_launch_gemv_mma_nvfp4_preq_fast": (I, [P, P, P, P, P, I, I, P]),
+    "vib3_launch_fused_swiglu_mma_nvfp4_preq": (I, [P, P, P, P, P, P, P, I, I, P]),
+    "vib3_launch_fused_swiglu_mma_nvfp4_preq_fast": (I, [P, P, P, P, P, P, P, I, I, P]),
+    "vib3_launch_gemv_mma_nvfp4_tiled": (I, [P, P, P, P, P, I, I, P]),
+    "vib3_launch_gemv_scalar_nvfp4": (I, [P, P, P, P, P, I, I, P]),
+    "vib3_launch_gemv_mma_nvfp4": (I, [P, P, P, P, I, I, P]),
+    "vib3_launch_fused_swiglu_mma_nvfp4": (I, [P, P, P, P, P, P, I, I, P]),
+    "vib3_launch_partial_matmul_nvfp4": (I, [P, P, P, P, I, I, I, P]),
+    "vib3_launch_partial_matmul_nvfp4_f32out": (I, [P, P, P, P, I, I, I, P]),
+    "vib3_launch_partial_matmul_nvfp4_fp16in": (I, [P, P, P, P, I, I, I, P]),
+    "vib3_launch_fused_swiglu_nvfp4": (I, [P, P, P, P, P, P, I, I, I, P]),
+    "vib3_launch_fused_swiglu_nvfp4_f32out": (I, [P, P, P, P, P, P, I, I, I, P]),
 }
 
 _lib = None

@@ -15,7 +15,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libvib3_hip.so")
 SOURCES = ["api.hip", "int4_gemv.hip", "router.hip", "synth.hip", "mxfp4_moe.hip", "norm.hip",
-           "vib3file.cpp", "fp4_fused.hip"]
+           "vib3file.cpp", "fp4_fused.hip", "fp4_pages.hip"]
 ARCH = os.environ.get("VIB3_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

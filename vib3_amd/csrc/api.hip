@@ -118,10 +118,10 @@ char* noalloc_scratch() {
 int router_mode(const vib3_moe_int4_layer* L) {
   if (!L->router_w || L->top_k <= 0) return kRouteGiven;
   int mode = L->num_experts <= kMaxExpertsInKernel ? 2 : 0;
-  if (const char* v = getenv("VIB3_ROUTE_MODE")) {
-    const int m = atoi(v);
-    if (m >= 0 && m <= 2) mode = L->num_experts <= kMaxExpertsInKernel ? m : 0;
-  }
+#ifdef VIB3_ROUTE_MODE  // (profiling builds: 0 separate selection launch, 1 selection from
+                        // the router kernel's scores in the gate/up prologue, 2 fused)
+  mode = L->num_experts <= kMaxExpertsInKernel ? VIB3_ROUTE_MODE : 0;
+#endif
   return mode == 2 ? kRouteFused : mode == 1 ? kRouteScores : kRouteGiven;
 }
 
@@ -409,9 +409,12 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only,
   // normalises x itself and computes the shared experts' gates where it can (fused routing,
   // f32 stream in int16 chunks, hidden <= 8192); else the prologue kernel writes RMSNorm(x)
   // and the gates first (stage 0 with the router).
-  const int x_i16 = getenv("VIB3_F32_SPLIT") ? 0 : 1;  // f32 stream: int16 chunks (A/B: split)
+#ifndef VIB3_F32_SPLIT
+#define VIB3_F32_SPLIT 0  // (profiling builds: f32 stream as hi + lo f16 pairs)
+#endif
+  const int x_i16 = VIB3_F32_SPLIT ? 0 : 1;  // f32 stream: int16 chunks
   bool fuse_prologue = false;
-  if (L->norm_weight && !getenv("VIB3_PROLOGUE_KERNEL")) {
+  if (L->norm_weight && !(L->flags & VIB3_MOE_SEPARATE_PROLOGUE)) {
     RowsArgs p{};
     p.x = L->x; p.x_dt = L->x_dtype; p.x_i16 = x_i16; p.K = L->hidden; p.M = L->inter;
     p.nslots = nslots; p.routed_table = L->page_table; p.route = router_mode(L);
@@ -499,7 +502,10 @@ static int moe_int4_layer(const vib3_moe_int4_layer* L, void* stream, int only,
   a.route = route;
   a.router = router;
   a.x_i16 = x_i16;
-  a.pre_shared = getenv("VIB3_PRE_SHARED") ? atoi(getenv("VIB3_PRE_SHARED")) : 1;  // (A/B knob)
+#ifndef VIB3_PRE_SHARED
+#define VIB3_PRE_SHARED 1  // (profiling builds: 0 = no shared items before the selection)
+#endif
+  a.pre_shared = VIB3_PRE_SHARED;
   if (fuse_prologue) {
     a.norm_w = (const uint16_t*)L->norm_weight;
     a.eps = L->norm_eps;

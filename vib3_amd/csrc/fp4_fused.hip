@@ -26,118 +26,11 @@
 #include <mutex>
 
 #include "common.h"
+#include "fp4.h"
 #include "kernels.h"
 
 namespace vib3 {
 namespace {
-
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-constexpr int kFp4MaxActive = 8;  // MOE_MAX_EXPERTS (kernels.cu:5331)
-#ifndef VIB3_FP4_DEPTH
-#define VIB3_FP4_DEPTH 2  // 1 KB tile pairs in flight per matrix stream (build-time knob)
-#endif
-constexpr int kFp4Depth = VIB3_FP4_DEPTH;
-
-// ------------------------------------------------------------------------- scalar pieces
-
-// E8M0 exponent of a group's scale from its absolute maximum (kernels.cu:2759-2768):
-// round(log2(amax)) - 2 + 127 clamped to [0, 254], with round(log2) taken exactly as
-// floor(log2) + (mantissa > sqrt 2) (the float just below sqrt 2 has mantissa 0x3504f3).
-__device__ __forceinline__ uint32_t e8m0_of_amax(float amax) {
-  if (!(amax > 0.0f)) return 0;
-  const uint32_t b = __float_as_uint(amax);
-  const int E = (int)(b >> 23);
-  if (E == 0) return 0;  // subnormal: log2 < -126, below the clamp
-  const int n = E - 127 + ((b & 0x7fffff) > 0x3504f3 ? 1 : 0);
-  const int biased = n + 125;
-  return (uint32_t)(biased < 0 ? 0 : biased > 254 ? 254 : biased);
-}
-
-// Round-to-nearest-even onto the E2M1 grid {0, .5, 1, 1.5, 2, 3, 4, 6}, saturating at 6,
-// sign kept (cvt.rn.satfinite semantics of __nv_fp4x4_e2m1, used at kernels.cu:3227).
-__device__ __forceinline__ uint32_t e2m1_rne(float v) {
-  const uint32_t sign = (__float_as_uint(v) >> 31) << 3;
-  const float a = fabsf(v);
-  uint32_t c;
-  if (a <= 0.25f) c = 0;
-  else if (a < 0.75f) c = 1;
-  else if (a <= 1.25f) c = 2;
-  else if (a < 1.75f) c = 3;
-  else if (a <= 2.5f) c = 4;
-  else if (a < 3.5f) c = 5;
-  else if (a <= 5.0f) c = 6;
-  else c = 7;
-  return sign | c;
-}
-
-// 1 / 2^(e - 127), the exact reciprocal of an E8M0 scale (e = 0 reads as 0 there, whose
-// reciprocal is +inf, kernels.cu:2770-2777 with __frcp_rn).
-__device__ __forceinline__ float e8m0_inv(uint32_t e) {
-  return e == 0 ? __builtin_huge_valf() : __uint_as_float((254u - e) << 23);
-}
-
-// e^x by Cody-Waite reduction x = n ln2 + r (ln2 split in a 15-bit head and a tail, so n * head
-// is exact) and the degree-7 Taylor polynomial of e^r on |r| <= ln2 / 2 in Horner form, then
-// ldexp. Every operation is a single IEEE rounding (no contraction), so the oracle's C version
-// gives the same bits; within 2 ulp of the correctly rounded exp (tested against libm).
-__device__ __forceinline__ float exp_cw(float x) {
-#pragma clang fp contract(off)
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return __builtin_huge_valf();
-  if (x < -103.97208404541015625f) return 0.0f;
-  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
-  float r = x - n * 0.693145751953125f;
-  r = r - n * 1.428606765330187045e-06f;
-  float p = 1.0f / 5040.0f;
-  p = p * r + 1.0f / 720.0f;
-  p = p * r + 1.0f / 120.0f;
-  p = p * r + 1.0f / 24.0f;
-  p = p * r + 1.0f / 6.0f;
-  p = p * r + 0.5f;
-  p = p * r + 1.0f;
-  p = p * r + 1.0f;
-  return __builtin_ldexpf(p, (int)n);
-}
-
-// h = (g * sigmoid(g)) * u, sigmoid(g) = 1 / (1 + e^-g), in the reference's order
-// (kernels.cu:5485-5487).
-__device__ __forceinline__ float swiglu_fp4(float g, float u) {
-#pragma clang fp contract(off)
-  const float sig = 1.0f / (1.0f + exp_cw(-g));
-  return (g * sig) * u;
-}
-
-// 2^(e) as a double for e in [-254, 254] (always a normal double: exact).
-__device__ __forceinline__ double pow2d(int e) {
-  return __longlong_as_double((long long)(e + 1023) << 52);
-}
-
-// Sixteen split-half bytes (one group) as sixteen f16 pairs (value j, value j + 16), exact.
-__device__ __forceinline__ void decode_group(const uint4 w, f16x2 (&o)[16]) {
-  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    o[4 * i + 0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 0);
-    o[4 * i + 1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 1);
-    o[4 * i + 2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 2);
-    o[4 * i + 3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wd[i], 1.0f, 3);
-  }
-}
-
-// Exact group dot product of weight bytes `w` with a decoded activation group in LDS.
-__device__ __forceinline__ float group_dot(const uint4 w, const uint4* act) {
-  const uint4 a4[4] = {act[0], act[1], act[2], act[3]};
-  const uint32_t aw[16] = {a4[0].x, a4[0].y, a4[0].z, a4[0].w, a4[1].x, a4[1].y, a4[1].z, a4[1].w,
-                           a4[2].x, a4[2].y, a4[2].z, a4[2].w, a4[3].x, a4[3].y, a4[3].z, a4[3].w};
-  f16x2 wp[16];
-  decode_group(w, wp);
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 16; j++)
-    s = __builtin_amdgcn_fdot2(wp[j], __builtin_bit_cast(f16x2, aw[j]), s, false);
-  return s;
-}
 
 // ------------------------------------------------------------------------- arguments
 
@@ -353,12 +246,6 @@ __device__ __forceinline__ void run_streams(PairStream<D> (&st)[NS], const uint4
   }
 }
 
-__device__ __forceinline__ double shfl_xor_d(double v, int m) {
-  const long long b = __double_as_longlong(v);
-  const int lo = __shfl_xor((int)(uint32_t)b, m), hi = __shfl_xor((int)(uint32_t)(b >> 32), m);
-  return __longlong_as_double(((long long)hi << 32) | (uint32_t)lo);
-}
-
 // ------------------------------------------------------------------------- kernels
 
 // Down projection + weighted combine, one workgroup per CU: wave w owns the four output rows
@@ -526,6 +413,28 @@ __global__ __launch_bounds__(256) void k_fp4_quant_act(const float* x, uint8_t* 
   const int g = i >> 5, j = i & 31;
   if (j < 16 && g * 32 + j < K) codes[(size_t)g * 16 + j] = (uint8_t)(code | (hi << 4));
   if (j == 0 && g * 32 < K) scales[g] = (uint8_t)e;
+}
+
+// Weight quantizer (kernels.cu:6017-6128): f16 [M][K] (K a multiple of 32, so every group lies
+// in one row and the groups of the flattened matrix are its rows' groups in order) to
+// row-major split-half E2M1 codes and bf16 scales holding the E8M0 exponent (e << 7), the
+// format of the block-scaled GEMV kernels. The same rule per group as k_fp4_quant_act.
+__global__ __launch_bounds__(256) void k_fp4_weight_quant(const uint16_t* w, uint8_t* codes,
+                                                          uint16_t* scales, long long n) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = lane_id();
+  const float v = i < n ? f16_to_f32(w[i]) : 0.0f;
+  float amax = fabsf(v);
+#pragma unroll
+  for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+  const uint32_t e = e8m0_of_amax(amax);
+  const float inv = amax == 0.0f ? 0.0f : e8m0_inv(e);
+  const uint32_t code = e2m1_rne(v * inv);
+  const uint32_t hi = (uint32_t)__shfl(code, (lane & ~31) + (lane & 15) + 16);
+  const long long g = i >> 5;
+  const int j = (int)(i & 31);
+  if (j < 16 && i < n) codes[g * 16 + j] = (uint8_t)(code | (hi << 4));
+  if (j == 0 && i < n) scales[g] = (uint16_t)(e << 7);
 }
 
 // Fused RMSNorm + FP4 quantizer (kernels.cu:6585-6702). Every workgroup forms the inverse RMS
@@ -853,16 +762,47 @@ int check_shape(int n, int K_in, int M_mid, int K_mid, int M_out) {
   return 0;
 }
 
-int launch_fused(Fp4Args& a, hipStream_t st) {
+int prewarm(int mid);
+
+// The slots' intermediate buffer: the caller's workspace (the _ws entry points), else the
+// device's buffer from vib3_moe_prewarm_gpu_bufs, allocated here on first use when the stream
+// is not being captured (as the reference's launchers do, kernels.cu:5675); under capture
+// without a prewarm, VIB3_ERR_WORKSPACE.
+int bind_mid(Fp4Args& a, hipStream_t st, void* ws, size_t ws_bytes) {
+  if (ws) {
+    const size_t stride = mid_stride(a.M_mid);
+    if (((uintptr_t)ws & 255) || ws_bytes < stride * kFp4MaxActive) return VIB3_ERR_WORKSPACE;
+    a.mid = (uint8_t*)ws;
+    a.mid_stride = stride;
+    return 0;
+  }
   const int dev = current_device();
   if (dev < 0) return VIB3_ERR_BAD_POINTER;
-  const MidBuf mb = g_mid[dev];
-  if (!mb.ptr || mb.max_mid < a.M_mid) return VIB3_ERR_WORKSPACE;  // not prewarmed
+  MidBuf mb;
+  {
+    std::lock_guard<std::mutex> lock(g_mid_lock);
+    mb = g_mid[dev];
+  }
+  if (!mb.ptr || mb.max_mid < a.M_mid) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return VIB3_ERR_WORKSPACE;
+    const int rc = prewarm(a.M_mid);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lock(g_mid_lock);
+    mb = g_mid[dev];
+  }
   a.mid = mb.ptr;
   a.mid_stride = mb.stride;
+  return 0;
+}
+
+int launch_fused(Fp4Args& a, hipStream_t st, void* ws = nullptr, size_t ws_bytes = 0) {
+  const int rc = bind_mid(a, st, ws, ws_bytes);
+  if (rc) return rc;
   hipLaunchKernelGGL(k_fp4_gateup, dim3((unsigned)(a.M_mid / 32), (unsigned)a.n), dim3(512),
                      (unsigned)gateup_lds(a.K_in), st, a);
-  if (a.M_mid % 512 == 0 && getenv("VIB3_FP4_DOWN_BLOCKS") == nullptr) {
+  if (a.M_mid % 512 == 0) {
     // one workgroup per CU, waves owning four output rows each
     const int G4 = a.M_out / 4;
     int wpb = (G4 + device_cus() - 1) / device_cus();
@@ -877,6 +817,23 @@ int launch_fused(Fp4Args& a, hipStream_t st) {
                        (unsigned)down_lds(a.n, a.M_mid), st, a);
   }
   VIB3_RETURN_LAUNCH();
+}
+
+int prewarm(int mid) {
+  const int dev = current_device();
+  if (dev < 0) return VIB3_ERR_BAD_POINTER;
+  std::lock_guard<std::mutex> lock(g_mid_lock);
+  MidBuf& mb = g_mid[dev];
+  if (mb.ptr && mb.max_mid >= mid) return 0;
+  const size_t stride = mid_stride(mid);
+  void* p = nullptr;
+  const hipError_t e = hipMalloc(&p, stride * kFp4MaxActive);
+  if (e != hipSuccess) return (int)e;
+  // the previous buffer stays allocated: a launch already queued may still read it
+  mb.ptr = (uint8_t*)p;
+  mb.stride = stride;
+  mb.max_mid = mid;
+  return 0;
 }
 
 }  // namespace
@@ -910,6 +867,19 @@ int vib3_launch_fused_rms_norm_quantize_fp4(const void* input, const void* norm_
   VIB3_RETURN_LAUNCH();
 }
 
+int vib3_launch_fp16_to_nvfp4_weight(const void* input, void* out_data, void* out_scales, int M,
+                                     int K, void* stream) {
+  if (M < 0 || K < 0) return VIB3_ERR_BAD_COUNT;
+  if (K % 32) return VIB3_ERR_UNSUPPORTED;  // whole groups per row (kernels.cu:6134)
+  if (!input || !out_data || !out_scales) return VIB3_ERR_BAD_POINTER;
+  const long long n = (long long)M * K;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_fp4_weight_quant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)input, (uint8_t*)out_data,
+                     (uint16_t*)out_scales, n);
+  VIB3_RETURN_LAUNCH();
+}
+
 int vib3_launch_quantize_activation_fp4_fast(const void* input, void* act_fp4, void* act_scales,
                                              int K, void* stream) {
   return vib3_launch_quantize_activation_fp4(input, act_fp4, act_scales, K, stream);
@@ -917,33 +887,23 @@ int vib3_launch_quantize_activation_fp4_fast(const void* input, void* act_fp4, v
 
 int vib3_moe_prewarm_gpu_bufs(int m_mid, int k_mid) {
   if (m_mid <= 0 || k_mid <= 0) return VIB3_ERR_BAD_COUNT;
-  const int mid = m_mid > k_mid ? m_mid : k_mid;
-  const int dev = current_device();
-  if (dev < 0) return VIB3_ERR_BAD_POINTER;
-  std::lock_guard<std::mutex> lock(g_mid_lock);
-  MidBuf& mb = g_mid[dev];
-  if (mb.ptr && mb.max_mid >= mid) return 0;
-  const size_t stride = mid_stride(mid);
-  void* p = nullptr;
-  const hipError_t e = hipMalloc(&p, stride * kFp4MaxActive);
-  if (e != hipSuccess) return (int)e;
-  // the previous buffer stays allocated: a launch already queued may still read it
-  mb.ptr = (uint8_t*)p;
-  mb.stride = stride;
-  mb.max_mid = mid;
-  return 0;
+  return prewarm(m_mid > k_mid ? m_mid : k_mid);
 }
 
-int vib3_launch_moe_experts_fused(const void* act_fp4, const void* act_scales,
-                                  const void* const* up_weight_ptrs,
-                                  const void* const* up_scale_ptrs,
-                                  const void* const* gate_weight_ptrs,
-                                  const void* const* gate_scale_ptrs,
-                                  const void* const* down_weight_ptrs,
-                                  const void* const* down_scale_ptrs,
-                                  const float* expert_weights_host, int num_experts, int K_in,
-                                  int M_mid, int K_mid, int M_out, float* layer_output,
-                                  void* stream) {
+size_t vib3_moe_experts_fused_workspace_bytes(int m_mid) {
+  return m_mid > 0 ? mid_stride(m_mid) * kFp4MaxActive : 0;
+}
+
+}  // extern "C"
+
+namespace {
+
+int fused_host(const void* act_fp4, const void* act_scales, const void* const* up_weight_ptrs,
+               const void* const* up_scale_ptrs, const void* const* gate_weight_ptrs,
+               const void* const* gate_scale_ptrs, const void* const* down_weight_ptrs,
+               const void* const* down_scale_ptrs, const float* expert_weights_host,
+               int num_experts, int K_in, int M_mid, int K_mid, int M_out, float* layer_output,
+               void* ws, size_t ws_bytes, void* stream) {
   const int rc = check_shape(num_experts, K_in, M_mid, K_mid, M_out);
   if (rc) return rc;
   if (!act_fp4 || !act_scales || !up_weight_ptrs || !up_scale_ptrs || !gate_weight_ptrs ||
@@ -962,14 +922,13 @@ int vib3_launch_moe_experts_fused(const void* act_fp4, const void* act_scales,
     a.mat[s][2] = Fp4Mat{(const uint8_t*)down_weight_ptrs[s], (const uint16_t*)down_scale_ptrs[s]};
     a.wts[s] = expert_weights_host[s];
   }
-  return launch_fused(a, (hipStream_t)stream);
+  return launch_fused(a, (hipStream_t)stream, ws, ws_bytes);
 }
 
-int vib3_launch_moe_experts_fused_gpu(const void* act_fp4, const void* act_scales,
-                                      const uint64_t* page_table, const uint16_t* expert_ids,
-                                      const float* expert_weights, int layer,
-                                      int num_experts_total, int num_active, int K_in, int M_mid,
-                                      int K_mid, int M_out, float* layer_output, void* stream) {
+int fused_dev(const void* act_fp4, const void* act_scales, const uint64_t* page_table,
+              const uint16_t* expert_ids, const float* expert_weights, int layer,
+              int num_experts_total, int num_active, int K_in, int M_mid, int K_mid, int M_out,
+              float* layer_output, void* ws, size_t ws_bytes, void* stream) {
   const int rc = check_shape(num_active, K_in, M_mid, K_mid, M_out);
   if (rc) return rc;
   if (layer < 0 || num_experts_total <= 0) return VIB3_ERR_BAD_COUNT;
@@ -986,7 +945,86 @@ int vib3_launch_moe_experts_fused_gpu(const void* act_fp4, const void* act_scale
   a.n = num_active;
   a.K_in = K_in; a.M_mid = M_mid; a.M_out = M_out;
   a.out = layer_output;
-  return launch_fused(a, (hipStream_t)stream);
+  return launch_fused(a, (hipStream_t)stream, ws, ws_bytes);
+}
+
+}  // namespace
+
+extern "C" {
+
+int vib3_launch_moe_experts_fused(const void* act_fp4, const void* act_scales,
+                                  const void* const* up_weight_ptrs,
+                                  const void* const* up_scale_ptrs,
+                                  const void* const* gate_weight_ptrs,
+                                  const void* const* gate_scale_ptrs,
+                                  const void* const* down_weight_ptrs,
+                                  const void* const* down_scale_ptrs,
+                                  const float* expert_weights_host, int num_experts, int K_in,
+                                  int M_mid, int K_mid, int M_out, float* layer_output,
+                                  void* stream) {
+  return fused_host(act_fp4, act_scales, up_weight_ptrs, up_scale_ptrs, gate_weight_ptrs,
+                    gate_scale_ptrs, down_weight_ptrs, down_scale_ptrs, expert_weights_host,
+                    num_experts, K_in, M_mid, K_mid, M_out, layer_output, nullptr, 0, stream);
+}
+
+int vib3_launch_moe_experts_fused_ws(const void* act_fp4, const void* act_scales,
+                                     const void* const* up_weight_ptrs,
+                                     const void* const* up_scale_ptrs,
+                                     const void* const* gate_weight_ptrs,
+                                     const void* const* gate_scale_ptrs,
+                                     const void* const* down_weight_ptrs,
+                                     const void* const* down_scale_ptrs,
+                                     const float* expert_weights_host, int num_experts, int K_in,
+                                     int M_mid, int K_mid, int M_out, float* layer_output,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (!workspace) return VIB3_ERR_BAD_POINTER;
+  return fused_host(act_fp4, act_scales, up_weight_ptrs, up_scale_ptrs, gate_weight_ptrs,
+                    gate_scale_ptrs, down_weight_ptrs, down_scale_ptrs, expert_weights_host,
+                    num_experts, K_in, M_mid, K_mid, M_out, layer_output, workspace,
+                    workspace_bytes, stream);
+}
+
+int vib3_launch_moe_experts_fused_gpu(const void* act_fp4, const void* act_scales,
+                                      const uint64_t* page_table, const uint16_t* expert_ids,
+                                      const float* expert_weights, int layer,
+                                      int num_experts_total, int num_active, int K_in, int M_mid,
+                                      int K_mid, int M_out, float* layer_output, void* stream) {
+  return fused_dev(act_fp4, act_scales, page_table, expert_ids, expert_weights, layer,
+                   num_experts_total, num_active, K_in, M_mid, K_mid, M_out, layer_output,
+                   nullptr, 0, stream);
+}
+
+int vib3_launch_moe_experts_fused_gpu_ws(const void* act_fp4, const void* act_scales,
+                                         const uint64_t* page_table, const uint16_t* expert_ids,
+                                         const float* expert_weights, int layer,
+                                         int num_experts_total, int num_active, int K_in,
+                                         int M_mid, int K_mid, int M_out, float* layer_output,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (!workspace) return VIB3_ERR_BAD_POINTER;
+  return fused_dev(act_fp4, act_scales, page_table, expert_ids, expert_weights, layer,
+                   num_experts_total, num_active, K_in, M_mid, K_mid, M_out, layer_output,
+                   workspace, workspace_bytes, stream);
+}
+
+int vib3_launch_expert_batched(const void* act_fp4, const void* act_scales,
+                               const void* up_weight, const void* up_scales,
+                               const void* gate_weight, const void* gate_scales,
+                               const void* down_weight, const void* down_scales,
+                               float* layer_output, float expert_weight, int K_in, int M_mid,
+                               int K_mid, int M_out, void* stream) {
+  // kernels.cu:4708: one expert's up, gate, SwiGLU, FP4 quantization of h, down and
+  // layer_output += expert_weight * down, over tiled split-half pages; the fused pipeline with
+  // one active expert computes exactly that
+  const void* up[1] = {up_weight};
+  const void* us[1] = {up_scales};
+  const void* gt[1] = {gate_weight};
+  const void* gs[1] = {gate_scales};
+  const void* dn[1] = {down_weight};
+  const void* ds[1] = {down_scales};
+  if (!up_weight || !up_scales || !gate_weight || !gate_scales || !down_weight || !down_scales)
+    return VIB3_ERR_BAD_POINTER;
+  return fused_host(act_fp4, act_scales, up, us, gt, gs, dn, ds, &expert_weight, 1, K_in,
+                    M_mid, K_mid, M_out, layer_output, nullptr, 0, stream);
 }
 
 int vib3_launch_repack_weights_inplace(void* weight_data_ptr, long long weight_data_bytes,

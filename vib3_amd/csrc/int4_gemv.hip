@@ -455,7 +455,8 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     // waves that share this SIMD
     __builtin_amdgcn_s_setprio(3);
     if (a.route == kRouteFused) {
-      select_topk_published_small(a.router, s_sel, s_wts, blockIdx.x == 0);
+      select_topk_published_small(a.router, s_sel, s_wts, blockIdx.x == 0,
+                                  NORM ? a.norm_w : nullptr, inv);
     } else if (a.route == kRouteScores) {
       select_topk_small(a.router, a.router.scores, s_sel, s_wts, blockIdx.x == 0);
     } else if (lane < top_k) {
@@ -1133,12 +1134,23 @@ static int pick_nch(int cpr, int max_ks, int& nch, int& ks) {
   return ks <= max_ks ? 0 : VIB3_ERR_UNSUPPORTED;
 }
 
-// Resident-capacity cap on the number of 256-thread blocks; VIB3_ROWS_BLOCKS_PER_CU overrides
-// (tuning knob; streaming reads peak near 32 KB in flight per CU, not at full occupancy).
-static int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return v && atoi(v) > 0 ? atoi(v) : dflt;
-}
+// Launch-shape constants, fixed at build time (profiling builds may set them with -D):
+// workgroups per CU of k_int4_rows (streaming reads peak near 32 KB in flight per CU, not at
+// full occupancy), of k_down_combine (0: resident capacity), waves per k_down_rows workgroup
+// (0: from the row count), and k_down_combine instead of k_down_rows (1).
+#ifndef VIB3_ROWS_BLOCKS_PER_CU
+#define VIB3_ROWS_BLOCKS_PER_CU 2
+#endif
+#ifndef VIB3_DOWN_BLOCKS_PER_CU
+#define VIB3_DOWN_BLOCKS_PER_CU 0
+#endif
+#ifndef VIB3_DOWN_WAVES
+#define VIB3_DOWN_WAVES 0
+#endif
+#ifndef VIB3_DOWN_COMBINE
+#define VIB3_DOWN_COMBINE 0
+#endif
+static int knob(int v, int dflt) { return v > 0 ? v : dflt; }
 
 template <int N, bool D, int S, bool P>
 static int rows_grid(const RowsArgs& a) {  // workgroups of a k_int4_rows launch
@@ -1148,7 +1160,7 @@ static int rows_grid(const RowsArgs& a) {  // workgroups of a k_int4_rows launch
   int cap = resident_blocks(k, 256);
   // At most two workgroups per CU: with a third, the CU serves the youngest last and it ends
   // the launch alone (c1: gate/up 26.4 -> 25.0 us with two)
-  const int per_cu = env_int("VIB3_ROWS_BLOCKS_PER_CU", 2);
+  const int per_cu = knob(VIB3_ROWS_BLOCKS_PER_CU, 2);
   if (per_cu * device_cus() < cap) cap = per_cu * device_cus();
   const int floor_blocks = (items + 4 * kWave - 1) / (4 * kWave);  // <= 64 items per wave
   if (cap < floor_blocks) cap = floor_blocks;
@@ -1252,7 +1264,7 @@ static void launch_down_t(DownArgs& a, hipStream_t s, KTime t) {
   auto k = k_down_combine<S, W>;
   const int block = a.nslots * a.KS * kWave;
   int cap = resident_blocks(k, block);
-  const int per_cu = env_int("VIB3_DOWN_BLOCKS_PER_CU", 0);
+  const int per_cu = knob(VIB3_DOWN_BLOCKS_PER_CU, 0);
   if (per_cu > 0 && per_cu * device_cus() < cap) cap = per_cu * device_cus();
   // rows per block: spread the rows evenly over the resident workgroups, a multiple of the
   // 8-row batch, at most 64 (one LDS column per row)
@@ -1281,7 +1293,7 @@ static void launch_down_rows_t(DownArgs& a, hipStream_t s, KTime t) {
   // (2..8): every CU streams the same share of the weights, and stages the activations once.
   // (Four-wave workgroups left some CUs two workgroups and others one.)
   const int groups = (a.M + R - 1) / R;
-  int wpb = env_int("VIB3_DOWN_WAVES", (groups + device_cus() - 1) / device_cus());
+  int wpb = knob(VIB3_DOWN_WAVES, (groups + device_cus() - 1) / device_cus());
   wpb = wpb < 2 ? 2 : wpb > 8 ? 8 : wpb;
   const int blocks = (groups + wpb - 1) / wpb;
   const int chunks = ONE ? kWave / R * J : a.K / 32;
@@ -1309,7 +1321,7 @@ int launch_down(DownArgs a, hipStream_t s, KTime t) {
   const int L = kWave / R;  // the LDS holds one pass's chunks (padded) or all cpr
   const int chunks = cpr <= L ? L : cpr <= 2 * L ? 2 * L : cpr <= 4 * L ? 4 * L : cpr;
   if (a.h_dt == VIB3_DT_F16 && down_rows_lds(a.nslots, chunks) <= 64 * 1024 &&
-      env_int("VIB3_DOWN_COMBINE", 0) == 0) {
+      VIB3_DOWN_COMBINE == 0) {
     if (R == 4) launch_down_rows_j<4>(a, cpr, s, t);
     else if (R == 2) launch_down_rows_j<2>(a, cpr, s, t);
     else launch_down_rows_j<1>(a, cpr, s, t);

@@ -1007,7 +1007,10 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   const unsigned items = (unsigned)mx_max_items(B);
   std::unique_lock<std::mutex> lock(g_mx_side_lock, std::defer_lock);
   MxSide* side = nullptr;
-  if (!getenv("VIB3_MX_ONE_STREAM")) {
+#ifndef VIB3_MX_ONE_STREAM
+#define VIB3_MX_ONE_STREAM 0  // (profiling builds: 1 = the three chains on the caller's stream)
+#endif
+  if (!VIB3_MX_ONE_STREAM) {
     lock.lock();
     side = mx_side();
   }

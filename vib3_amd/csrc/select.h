@@ -7,6 +7,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "norm.h"
 
 #ifdef VIB3_TRACE_SELECT  // (profiling builds: probes inside the selection too)
 #define VIB3_TRACE_FINE(k) VIB3_TRACE_POINT(k)
@@ -308,9 +309,26 @@ __device__ inline void select_topk_regs(const RouterArgs& a, const float* scores
 #endif
 constexpr int kPollGap = VIB3_POLL_GAP;
 
+// Logit of router row e computed by one wave (64 lanes over d, then a wave sum), for a wait
+// that gave up: x is the router's activation, or RMSNorm(x) with weights nw and inverse RMS
+// inv (the fused sublayer prologue). Its summation order is not the workgroup's, so the value
+// can differ from the published one in the last bits.
+__device__ inline float wave_row_dot(const RouterArgs& a, int e, const uint16_t* nw, float inv) {
+  const int lane = lane_id();
+  const size_t row = (size_t)e * a.D;
+  float acc = 0.0f;
+  for (int d = lane; d < a.D; d += kWave) {
+    float x = load_act(a.x, a.x_dt, d);
+    if (nw) x = norm_mul(x, inv, f16_to_f32(nw[d]));
+    acc = __builtin_fmaf(x, load_act(a.w, a.w_dt, row + d), acc);
+  }
+  return wave_sum(acc);
+}
+
 template <int R>
 __device__ inline void select_topk_published(const RouterArgs& a, int* sel, float* selv,
-                                             bool publish) {
+                                             bool publish, const uint16_t* nw = nullptr,
+                                             float inv = 1.0f) {
   const int lane = lane_id();
   float sc[R], bs[R];
   load_bias<R>(a, bs);  // before the wait, off the critical path
@@ -334,6 +352,7 @@ __device__ inline void select_topk_published(const RouterArgs& a, int* sel, floa
 #pragma unroll
     for (int r = 0; r < R; r++) sc[r] = __uint_as_float((uint32_t)v[r]);
   };
+  uint32_t missing = 0;  // bit r: this lane's expert lane + 64 r was never published
   issue(va);
   __builtin_amdgcn_s_sleep(kPollGap);
   issue(vb);
@@ -343,8 +362,14 @@ __device__ inline void select_topk_published(const RouterArgs& a, int* sel, floa
       break;
     }
     if (it >= a.spin_limit) {
+      // The wait gave up (reported through the status word): the logits not yet published
+      // are computed here from the router weights, so the selection still sees every expert
+      // and every workgroup selects the same ones.
       if (lane == 0) a.error[0] = 1;
       take(va);
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        missing |= (lane + r * kWave < a.E && (uint32_t)(va[r] >> 32) != want) ? 1u << r : 0u;
       break;
     }
     issue(va);
@@ -354,15 +379,28 @@ __device__ inline void select_topk_published(const RouterArgs& a, int* sel, floa
     }
     issue(vb);
   }
+  if (__ballot(missing != 0)) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      uint64_t m = __ballot((missing >> r) & 1u);
+      while (m) {
+        const int l = (int)__builtin_ctzll(m);
+        m &= m - 1;
+        const float v = wave_row_dot(a, l + r * kWave, nw, inv);
+        if (lane == l) sc[r] = v;
+      }
+    }
+  }
   select_topk_vals<R>(a, sc, bs, sel, selv, publish);
 }
 
 __device__ inline void select_topk_published_small(const RouterArgs& a, int* sel, float* selv,
-                                                   bool publish) {
-  if (a.E <= 2 * kWave) select_topk_published<2>(a, sel, selv, publish);
-  else if (a.E <= 4 * kWave) select_topk_published<4>(a, sel, selv, publish);
-  else if (a.E <= 6 * kWave) select_topk_published<6>(a, sel, selv, publish);
-  else select_topk_published<8>(a, sel, selv, publish);
+                                                   bool publish, const uint16_t* nw = nullptr,
+                                                   float inv = 1.0f) {
+  if (a.E <= 2 * kWave) select_topk_published<2>(a, sel, selv, publish, nw, inv);
+  else if (a.E <= 4 * kWave) select_topk_published<4>(a, sel, selv, publish, nw, inv);
+  else if (a.E <= 6 * kWave) select_topk_published<6>(a, sel, selv, publish, nw, inv);
+  else select_topk_published<8>(a, sel, selv, publish, nw, inv);
 }
 
 // Register selection for up to 8 * 64 experts, with the register count matched to E.

@@ -327,6 +327,118 @@ def moe_experts_fused_gpu(act_fp4: torch.Tensor, act_scales: torch.Tensor,
               _dev(layer_output, "layer_output"), _stream(layer_output))
 
 
+def _page_scales(page: torch.Tensor, k: int, m_slice: int) -> int:
+    """Device address of a page's scales: after its packed codes (kernels.rs:821-860)."""
+    return _dev(page, "page") + _nvfp4_data_bytes(k, m_slice)
+
+
+def _need_f32(t: torch.Tensor, name: str) -> None:
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name} must be an f32 tensor")
+
+
+def gemv_mma_nvfp4_preq(act_fp4: torch.Tensor, act_scales: torch.Tensor,
+                        weight_page: torch.Tensor, output: torch.Tensor, k: int,
+                        m_slice: int) -> None:
+    """kernels.rs:821 gemv_mma_nvfp4_preq: pre-quantized activation times a row-major
+    split-half NVFP4 page -> f32 [m_slice] (also :1200 gemv_mma_nvfp4_preq_fast)."""
+    _need_f32(output, "output")
+    _lib.call("vib3_launch_gemv_mma_nvfp4_preq", _dev(act_fp4, "act_fp4"),
+              _dev(act_scales, "act_scales"), _dev(weight_page, "weight_page"),
+              _page_scales(weight_page, k, m_slice), _dev(output, "output"), k, m_slice,
+              _stream(output))
+
+
+gemv_mma_nvfp4_preq_fast = gemv_mma_nvfp4_preq
+
+
+def fused_swiglu_mma_nvfp4_preq(act_fp4: torch.Tensor, act_scales: torch.Tensor,
+                                up_page: torch.Tensor, gate_page: torch.Tensor,
+                                output: torch.Tensor, k: int, m_slice: int) -> None:
+    """kernels.rs:862 fused_swiglu_mma_nvfp4_preq: (g * sigmoid(g)) * u of two page GEMVs,
+    f32 [m_slice] (also :1520 fused_swiglu_mma_nvfp4_preq_fast)."""
+    _need_f32(output, "output")
+    _lib.call("vib3_launch_fused_swiglu_mma_nvfp4_preq", _dev(act_fp4, "act_fp4"),
+              _dev(act_scales, "act_scales"), _dev(up_page, "up_page"),
+              _page_scales(up_page, k, m_slice), _dev(gate_page, "gate_page"),
+              _page_scales(gate_page, k, m_slice), _dev(output, "output"), k, m_slice,
+              _stream(output))
+
+
+fused_swiglu_mma_nvfp4_preq_fast = fused_swiglu_mma_nvfp4_preq
+
+
+def gemv_mma_nvfp4(input: torch.Tensor, weight_page: torch.Tensor, output: torch.Tensor,
+                   k: int, m_slice: int) -> None:
+    """kernels.rs:696 gemv_mma_nvfp4: f32 input (quantized to FP4 in the kernel) times a
+    sequential-nibble NVFP4 page -> f32."""
+    _need_f32(input, "input")
+    _need_f32(output, "output")
+    _lib.call("vib3_launch_gemv_mma_nvfp4", _dev(input, "input"), _dev(weight_page, "weight_page"),
+              _page_scales(weight_page, k, m_slice), _dev(output, "output"), k, m_slice,
+              _stream(output))
+
+
+def fused_swiglu_mma_nvfp4(input: torch.Tensor, up_page: torch.Tensor, gate_page: torch.Tensor,
+                           output: torch.Tensor, k: int, m_slice: int) -> None:
+    """kernels.rs:742 fused_swiglu_mma_nvfp4."""
+    _need_f32(input, "input")
+    _need_f32(output, "output")
+    _lib.call("vib3_launch_fused_swiglu_mma_nvfp4", _dev(input, "input"), _dev(up_page, "up_page"),
+              _page_scales(up_page, k, m_slice), _dev(gate_page, "gate_page"),
+              _page_scales(gate_page, k, m_slice), _dev(output, "output"), k, m_slice,
+              _stream(output))
+
+
+def partial_matmul_nvfp4_f32(input: torch.Tensor, weight_page: torch.Tensor,
+                             output: torch.Tensor, k: int, m_slice: int) -> None:
+    """kernels.rs:652 partial_matmul_nvfp4_f32: f32 input times a sequential NVFP4 page with
+    bf16 block scales, f32 output (vib3_launch_partial_matmul_nvfp4_f32out, block 32)."""
+    _need_f32(input, "input")
+    _need_f32(output, "output")
+    _lib.call("vib3_launch_partial_matmul_nvfp4_f32out", _dev(input, "input"),
+              _dev(weight_page, "weight_page"), _page_scales(weight_page, k, m_slice),
+              _dev(output, "output"), k, m_slice, 32, _stream(output))
+
+
+def partial_swiglu_f32_f32out(input: torch.Tensor, up_page: torch.Tensor,
+                              gate_page: torch.Tensor, output: torch.Tensor, hidden_dim: int,
+                              m_slice: int) -> None:
+    """kernels.rs:604 partial_swiglu_f32_f32out (NVFP4 pages): silu(g) * u in f32."""
+    _need_f32(input, "input")
+    _need_f32(output, "output")
+    _lib.call("vib3_launch_fused_swiglu_nvfp4_f32out", _dev(input, "input"),
+              _dev(up_page, "up_page"), _page_scales(up_page, hidden_dim, m_slice),
+              _dev(gate_page, "gate_page"), _page_scales(gate_page, hidden_dim, m_slice),
+              _dev(output, "output"), hidden_dim, m_slice, 32, _stream(output))
+
+
+def expert_batched(act_fp4: torch.Tensor, act_scales: torch.Tensor, up_page: torch.Tensor,
+                   gate_page: torch.Tensor, down_page: torch.Tensor, layer_output: torch.Tensor,
+                   expert_weight: float, k_in: int, m_mid: int, m_out: int) -> None:
+    """kernels.rs:947 expert_batched: one expert over tiled split-half pages, layer_output
+    (f32 [m_out]) += expert_weight * down(quantized SwiGLU(up, gate))."""
+    _need_f32(layer_output, "layer_output")
+    _lib.call("vib3_launch_expert_batched", _dev(act_fp4, "act_fp4"),
+              _dev(act_scales, "act_scales"), _dev(up_page, "up_page"),
+              _page_scales(up_page, k_in, m_mid), _dev(gate_page, "gate_page"),
+              _page_scales(gate_page, k_in, m_mid), _dev(down_page, "down_page"),
+              _page_scales(down_page, m_mid, m_out), _dev(layer_output, "layer_output"),
+              float(expert_weight), k_in, m_mid, m_mid, m_out, _stream(layer_output))
+
+
+def fp16_to_nvfp4_weight(input: torch.Tensor, m: int, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """kernels.rs:1161 fp16_to_nvfp4_weight: f16 [m, k] -> (row-major split-half codes
+    [m * k / 2], bf16 E8M0 scales [m * k / 32])."""
+    if input.dtype != torch.float16:
+        raise TypeError("fp16_to_nvfp4_weight takes an f16 tensor")
+    data = torch.empty(m * k // 2, dtype=torch.uint8, device=input.device)
+    scales = torch.empty(m * k // 32, dtype=torch.int16, device=input.device)
+    _lib.call("vib3_launch_fp16_to_nvfp4_weight", _dev(input, "input"), _dev(data, "data"),
+              _dev(scales, "scales"), m, k, _stream(input))
+    return data, scales
+
+
 def repack_weights_inplace(weight_data: torch.Tensor, weight_data_bytes: int) -> None:
     """kernels.rs:915: sequential -> split-half nibble order, in place."""
     _lib.call("vib3_launch_repack_weights_inplace", _dev(weight_data, "weight_data"),
