@@ -250,9 +250,21 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
   // every workgroup, which stream them while wave 0 waits for the routing (after their
   // workgroup's router row), and every wave takes the routed items S + it0 + k * stride after
   // them: the stream that waits for the selection is one item shorter.
-  const int NP = (int)gridDim.x * 3, S = (nslots - top_k) * M;
-  const bool pre = a.pre_shared && wave >= 1;
-  const int u = (int)blockIdx.x * 3 + wave - 1;
+  // Workgroups b and b + G/2 share a CU (dispatch order). Where both compute a router row
+  // (E > G/2), the second one selects on its third wave (the first selects on wave 0: the two
+  // selections run on different SIMDs) and takes no shared items before the selection (its
+  // polls then do not queue behind six streaming waves); the shared items go to the others.
+  const int Gh = G / 2;
+  const bool two_router = fused && E > Gh;
+  const bool second = (int)blockIdx.x >= Gh;
+  const int selw = (two_router && second) ? 2 : 0;   // the selecting wave
+  const int pw = wave < selw ? wave : wave - 1;       // rank among the other three
+  const bool no_pre = two_router && second && (int)blockIdx.x < E;
+  const int nwg = two_router ? Gh + max(0, G - E) : G;  // workgroups taking shared items
+  const int rk = (two_router && second) ? (int)blockIdx.x - (E - Gh) : (int)blockIdx.x;
+  const int NP = nwg * 3, S = (nslots - top_k) * M;
+  const bool pre = a.pre_shared && wave != selw && !no_pre;
+  const int u = rk * 3 + pw;
   const int cs = pre ? max(0, (S - u + NP - 1) / max(NP, 1)) : 0;  // this wave's shared items
   const int rbase = a.pre_shared ? S + it0 : it0;
   auto item_at = [&](int k) { return k < cs ? u + k * NP : rbase + (k - cs) * stride; };
@@ -318,7 +330,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     kres++;
   };
   const bool have = item_at(0) < items;
-  if (PAGED && wave == 0 && lane < nslots && lane >= top_k) {
+  if (PAGED && wave == selw && lane < nslots && lane >= top_k) {
     s_tab[lane][0] = shared_table_of(lane, 0);
     s_tab[lane][1] = shared_table_of(lane, 1);
   }
@@ -450,7 +462,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
     }
   }
   VIB3_TRACE_POINT(1);
-  if (PAGED && top_k > 0 && wave == 0) {
+  if (PAGED && top_k > 0 && wave == selw) {
     // the selection is on every routed row's critical path: issue ahead of the streaming
     // waves that share this SIMD
     __builtin_amdgcn_s_setprio(3);
@@ -513,7 +525,7 @@ __global__ __launch_bounds__(256) void k_int4_rows(RowsArgs a) {
                                    : a.shared_table + ((size_t)(sl - top_k) * 3 + 2) * a.max_pages;
     return t + p;
   };
-  const int pl_i = wave == 0 ? (int)blockIdx.x * kWave + lane : npl;
+  const int pl_i = wave == selw ? (int)blockIdx.x * kWave + lane : npl;
   uint64_t pl_v = 0;
   if (pl_i < npl) {
     for (int i = pl_i + G * kWave; i < npl; i += G * kWave) a.down_bases[i] = *(gtab*)pl_entry(i);
