@@ -224,3 +224,35 @@ def test_fused_rms_norm_quantize_known_answer_and_composition():
     c1, s1, h1 = O.fused_rms_norm_quantize_fp4(x, w.view(np.uint16), 1e-6, f16_out=True)
     assert np.array_equal(c1, c2) and np.array_equal(s1, s2)
     assert np.array_equal(h1, y.astype(np.float16).view(np.uint16))
+
+
+def test_exact_sums_stay_within_the_f32_accumulation_bound():
+    """The reference's MMA kernels accumulate each row's 64-value tile products in f32 in
+    tile order (kernels.cu:3276-3385, :4544-4700); this build and its oracle sum exactly and
+    round once. The two differ by at most the f32 accumulation bound n * 2^-24 * sum |tile|,
+    so any drift from the reference's numbers is bounded (observed: ~1e-7 relative)."""
+    rng = np.random.default_rng(17)
+    m, k = 64, 7168
+    x = rng.normal(0, 2, k).astype(np.float32)
+    codes, sc = O.fp4_quantize_act(x)
+    data = rng.integers(0, 256, m * k // 2, dtype=np.uint8)
+    ws = ((rng.integers(119, 124, (m, k // 32)) << 7)).astype(np.uint16)
+    exact = O.nvfp4_page_matvec(codes, sc, data, ws, m, k, 0).astype(np.float64)
+    g = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0., -.5, -1, -1.5, -2, -3, -4, -6])
+    a = np.concatenate([np.concatenate([g[c & 15] for c in codes.reshape(-1, 16)[i:i + 1]] +
+                                       [g[c >> 4] for c in codes.reshape(-1, 16)[i:i + 1]])
+                        for i in range(k // 32)])
+    a = a * np.repeat(2.0 ** (sc.astype(np.float64) - 127), 32)
+    worst = 0.0
+    for r in range(m):
+        row = data[r * k // 2:(r + 1) * k // 2].reshape(-1, 16)
+        w = np.concatenate([np.concatenate([g[b & 15], g[b >> 4]]) for b in row])
+        w = w * np.repeat(2.0 ** (((ws[r].astype(np.int64) >> 7) & 0xFF) - 127), 32)
+        tiles = (w * a).reshape(-1, 64).sum(1)           # each tile's sum: exact in f64
+        acc = np.float32(0.0)
+        for t in tiles:                                   # f32 accumulation in tile order
+            acc = np.float32(acc + np.float32(t))
+        bound = len(tiles) * 2.0 ** -24 * np.abs(tiles).sum() + 2.0 ** -24 * abs(exact[r])
+        assert abs(float(acc) - exact[r]) <= bound
+        worst = max(worst, abs(float(acc) - exact[r]) / max(np.abs(tiles).sum(), 1e-30))
+    assert worst < 1e-5
