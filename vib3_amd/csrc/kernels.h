@@ -44,8 +44,10 @@ struct RouterArgs {
   int* error;          // set to 1 if a wait gave up
 };
 
-// Polls of the fused router's bounded wait before it gives up and records an error.
-constexpr int kRouterSpinLimit = 1 << 20;
+// Polls of the fused router's bounded wait before it gives up, records an error and computes
+// the logits it has not seen itself (a poll round is one device round trip, ~1-2 us, so the
+// limit is tens of milliseconds; a wait normally ends within a few rounds).
+constexpr int kRouterSpinLimit = 1 << 15;
 
 // Device tags are 31-bit and never 0; host-side stage tags set bit 31, so the two never meet.
 __host__ __device__ inline uint32_t next_tag(uint32_t g) {

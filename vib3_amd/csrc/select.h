@@ -302,7 +302,8 @@ __device__ inline void select_topk_regs(const RouterArgs& a, const float* scores
 // workgroup that computed it), then select. Tags make the wait independent of any ordering
 // between different addresses, so no device-wide fence is needed. The wait is bounded: after
 // RouterArgs::spin_limit polls (kRouterSpinLimit normally) the wave records an error, which
-// the host reads with vib3_moe_int4_layer_status, and selects from what it has.
+// the host reads with vib3_moe_int4_layer_status, computes the logits it has not seen from the
+// router weights, and selects from the complete set.
 
 #ifndef VIB3_POLL_GAP
 #define VIB3_POLL_GAP 20  // s_sleep units (64 clocks) between the two poll rounds in flight
