@@ -86,11 +86,13 @@ def test_synth_mxfp4_page_device_matches_oracle():
 
 @pytest.mark.parametrize("hidden,inter,E,T,k", [(256, 256, 12, 5, 3), (512, 768, 9, 37, 4),
                                                  (256, 256, 3, 70, 2), (2560, 6144, 12, 5, 3),
-                                                 (6144, 2560, 6, 9, 2), (4096, 4096, 8, 6, 2)])
+                                                 (6144, 2560, 6, 9, 2), (4096, 4096, 8, 6, 2),
+                                                 (512, 512, 3, 70, 2), (1024, 512, 6, 130, 3)])
 def test_small_batches_match_oracle(hidden, inter, E, T, k):
-    """Shapes with 1..70 tokens per expert (row path, several 16-token matrix-core blocks, a
+    """Shapes with 1..70+ tokens per expert (row path, several 16-token matrix-core blocks, a
     64-token chunk and a remainder), experts picked twice by one token, experts never picked,
-    and reduction lengths that give the row path 1, 2, 3 and 4 chunks per lane."""
+    and reduction lengths that give the row path 1, 2, 3 and 4 chunks per lane. k multiples of
+    512 take the LDS-staged matrix-core kernel, the others the registers-only one."""
     _say(f"[mxfp4] small hidden={hidden} inter={inter} E={E} T={T} k={k}")
     from vib3_amd.mxfp4 import zipf_picks
     bank = _bank(hidden, inter, E)

@@ -895,6 +895,10 @@ struct MxSide {
 #define VIB3_MX_THREE_STREAMS 1  // (build-time switch: the two row paths on streams of their own)
 #endif
 constexpr bool kMxThreeStreams = VIB3_MX_THREE_STREAMS;
+// The fork and join events order work of one device only: device-scope fences suffice, and
+// skipping the system-scope ones (cache write-back and invalidation at each event) took ~4.5 us
+// off a c4 batch.
+constexpr unsigned kMxEventFlags = hipEventDisableTiming | hipEventDisableSystemFence;
 static MxSide g_mx_side[64];
 static std::mutex g_mx_side_lock;
 
@@ -906,9 +910,9 @@ static MxSide* mx_side() {  // called with the lock held
     if (hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&s.st2, hipStreamNonBlocking) != hipSuccess)
       return nullptr;
-    if (hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&s.join2, hipEventDisableTiming) != hipSuccess)
+    if (hipEventCreateWithFlags(&s.fork, kMxEventFlags) != hipSuccess ||
+        hipEventCreateWithFlags(&s.join, kMxEventFlags) != hipSuccess ||
+        hipEventCreateWithFlags(&s.join2, kMxEventFlags) != hipSuccess)
       return nullptr;
     s.ok = true;
   }
@@ -925,6 +929,19 @@ struct MxWs {
 static int mx_max_items(const vib3_moe_mxfp4_batch* B) {
   const int n = B->tokens * B->top_k;
   return n / kMxTokBlk + 2 * ((B->num_experts < n ? B->num_experts : n) + n / kMxChunk);
+}
+
+// Grid rows of the matrix-core launches: the work items k_mx_group can form. Each expert there
+// has more than kMxColdMax entries and takes ceil(entries / kMxTokBlk) items, so at most
+// (n + (kMxTokBlk - 1) m) / kMxTokBlk for m = min(E, n / (kMxColdMax + 1)) such experts. (A
+// workgroup past the last item returns at once, but every one of them is still dispatched.)
+static int mx_grid_items(const vib3_moe_mxfp4_batch* B) {
+  const int n = B->tokens * B->top_k;
+  const int hot = n / (kMxColdMax + 1);
+  const int m = B->num_experts < hot ? B->num_experts : hot;
+  const int bound = (n + (kMxTokBlk - 1) * m) / kMxTokBlk;
+  const int cap = mx_max_items(B);
+  return bound < cap ? bound : cap;
 }
 
 static MxWs mx_ws(const vib3_moe_mxfp4_batch* B) {
@@ -1004,7 +1021,7 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   a.c_dix = ga.c_dix; a.ncold = ga.ncold; a.ncold1 = ga.ncold1;
   a.h = (uint16_t*)(ws + w.h); a.d = (uint16_t*)(ws + w.d);
   a.hidden = B->hidden; a.inter = B->inter;
-  const unsigned items = (unsigned)mx_max_items(B);
+  const unsigned items = (unsigned)mx_grid_items(B);
   std::unique_lock<std::mutex> lock(g_mx_side_lock, std::defer_lock);
   MxSide* side = nullptr;
 #ifndef VIB3_MX_ONE_STREAM
@@ -1027,14 +1044,16 @@ int vib3_launch_moe_mxfp4_batched(const vib3_moe_mxfp4_batch* B, void* stream) {
   mx_launch_rows<false>(a, B->inter, rs, rs2);
   // matrix-core path: activations staged in LDS when k is a multiple of the step, otherwise
   // registers-only with k split over the waves (gate/up) or whole (down)
-  if (B->hidden % kMx2K == 0)
+  if (items == 0) {  // (no expert can take the matrix-core path)
+  } else if (B->hidden % kMx2K == 0)
     hipLaunchKernelGGL((k_mx_gemm2<true, kMx2K>), dim3((unsigned)(B->inter / (16 * kMx2H)), items),
                        dim3(64 * kMx2W), 0,
                        st, a);
   else
     hipLaunchKernelGGL((k_mx_gemm<true, 4>), dim3((unsigned)(B->inter / 32), items), dim3(256), 0,
                        st, a);
-  if (B->inter % kMx2KD == 0)
+  if (items == 0) {
+  } else if (B->inter % kMx2KD == 0)
     hipLaunchKernelGGL((k_mx_gemm2<false, kMx2KD>), dim3((unsigned)(B->hidden / (16 * kMx2W)), items),
                        dim3(64 * kMx2W),
                        0, st, a);
