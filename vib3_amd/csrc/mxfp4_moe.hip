@@ -665,7 +665,9 @@ __host__ __device__ inline int mx_expert_items(int c) {
   return n;
 }
 
-// Group the T*top_k picks by expert (one workgroup). Entries of an expert keep pick order.
+// Group the T*top_k picks by expert (one workgroup). An expert's entries sit in the order its
+// counting atomic handed out places: not fixed, and no result depends on it (a token's products
+// are formed in its own MFMA column or GEMV lane whatever its place; the combine reads by pick).
 // Work items for the GEMM kernels are (distinct expert, 16-token slice of its entries).
 struct MxGroupArgs {
   const uint16_t* ids;  // [T*top_k]
@@ -697,8 +699,14 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
   for (int p = tid; p < a.n; p += nt) sid[p] = a.ids[p];
   __syncthreads();
   // picks with an id >= E are left out (the combine skips them too)
-  for (int p = tid; p < a.n; p += nt)
-    if (sid[p] < a.E) atomicAdd(&cnt[sid[p]], 1);
+  // the count's old value is the pick's place among its expert's entries (picks p = tid + k nt;
+  // the launch has nt = 1024 threads)
+  int myrank[kMxMaxPicks / 1024];
+#pragma unroll
+  for (int k = 0; k < kMxMaxPicks / 1024; k++) {
+    const int p = tid + k * nt;
+    myrank[k] = (p < a.n && sid[p] < a.E) ? atomicAdd(&cnt[sid[p]], 1) : 0;
+  }
   __syncthreads();
   // exclusive scans over experts of: entries, touched experts, work items. Thread tid owns a
   // contiguous span of experts.
@@ -781,23 +789,15 @@ __global__ __launch_bounds__(1024) void k_mx_group(MxGroupArgs a) {
   }
 
   __syncthreads();
-  // entry position = expert offset + number of earlier picks of the same expert (the earlier
-  // ids read eight at a time from the 16-byte aligned LDS copy, the last few one by one)
-  for (int p = tid; p < a.n; p += nt) {
+  // entry position = expert offset + the place the count handed out
+#pragma unroll
+  for (int k = 0; k < kMxMaxPicks / 1024; k++) {
+    const int p = tid + k * nt;
+    if (p >= a.n) break;
     const int e = sid[p];
     if (e >= a.E) continue;
-    int rank = 0;
-    const int p8 = p & ~7;
-    for (int q = 0; q < p8; q += 8) {
-      const uint4 v = *(const uint4*)(sid + q);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        rank += (int)((w[j] & 0xffffu) == (uint32_t)e) + (int)((w[j] >> 16) == (uint32_t)e);
-    }
-    for (int q = p8; q < p; q++) rank += sid[q] == e;
-    a.ent_tok[off[e] + rank] = p / a.top_k;
-    a.ent_slot[off[e] + rank] = p;
+    a.ent_tok[off[e] + myrank[k]] = p / a.top_k;
+    a.ent_slot[off[e] + myrank[k]] = p;
   }
 }
 
