@@ -295,6 +295,53 @@ def bench_c4(args, cfg) -> int:
     return 0
 
 
+def given_ids_pass(layers, xs, cfg, args, lib, st, nbytes) -> dict:
+    """The same layers with the experts given as ids (seeded picks, no router): the path the
+    reference engine takes after its own router launch, so the expert GEMVs run without the
+    routing window that the fused gate/up kernel spends computing and polling the logits.
+    Reported beside the headline, which is the fused layer; the roofline stays on the fused
+    kernel."""
+    import numpy as np
+    import torch
+
+    from vib3_amd import _hip, _lib
+
+    dev = xs[0].device
+    rng = np.random.default_rng(cfg["seed"] + 1)
+    gid = [torch.from_numpy(rng.choice(cfg["E"], cfg["k"], replace=False).astype(np.int16)).to(dev)
+           for _ in range(args.tokens)]
+    gw = torch.full((cfg["k"],), 1.0 / cfg["k"], dtype=torch.float32, device=dev)
+    descs = []
+    for ly in layers:
+        row = []
+        for t, x in enumerate(xs):
+            d = ly._desc(x, gid[t], gw)
+            d.router_w = None
+            row.append(d)
+        descs.append(row)
+    L = len(layers)
+    stage = {}
+    for j, name in ((1, "gateup"), (2, "down")):
+        for i in range(args.warmup):
+            lib.vib3_launch_moe_int4_layer(descs[i % L][i % args.tokens], st)
+        s0, s1 = _hip.Event(), _hip.Event()
+        s0.record(st)
+        for i in range(args.steps):
+            d = descs[i % L][i % args.tokens]
+            rc = lib.vib3_launch_moe_int4_layer_stage(d, j, st)
+            if rc:
+                raise _lib.Vib3Error("vib3_launch_moe_int4_layer_stage", rc)
+        s1.record(st)
+        s1.synchronize()
+        stage[name] = s0.elapsed_ms(s1) * 1e3 / args.steps
+    gu = nbytes["gateup"] / (stage["gateup"] * 1e-6) / 1e9
+    both = (nbytes["gateup"] + nbytes["down"]) / ((stage["gateup"] + stage["down"]) * 1e-6) / 1e9
+    return {"stages_us": {k: round(v, 3) for k, v in stage.items()},
+            "gateup_gbs": round(gu, 1), "gateup_frac": round(gu / HBM_PEAK_GBS, 4),
+            "gemv_gbs": round(both, 1), "gemv_frac": round(both / HBM_PEAK_GBS, 4),
+            "note": "seeded ids given (no router): the expert GEMV kernels alone"}
+
+
 def bench_fp4(args, cfg) -> int:
     """The reference's sync-free fused NVFP4 path: a step = quantize the f32 activation to FP4
     + vib3_launch_moe_experts_fused_gpu over 8 experts of a 384-expert layer (the launches the
@@ -529,6 +576,9 @@ def main() -> int:
         stage_us[name] = s0.elapsed_ms(s1) * 1e3 / args.steps
 
     nbytes = algorithmic_bytes(cfg, shape)
+    given = None
+    if fused and not args.sublayer:
+        given = given_ids_pass(layers, xs, cfg, args, lib, st, nbytes)
     if fused:  # the gate/up kernel also reads the router weights
         nbytes["gateup"] += nbytes["router"]
     gu_gbs = nbytes["gateup"] / (stage_us["gateup"] * 1e-6) / 1e9
@@ -607,6 +657,7 @@ def main() -> int:
         "settle": {"ms": args.settle_ms, "steps": n_settle},
         "layer_gbs": round(layer_gbs, 1),
         "expert_gemv_gbs": round(expert_gbs, 1),
+        "expert_gemv_given_ids": given,
         "copy_gbs": round(copy_gbs, 1) if copy_gbs else None,
         "cpu_baseline": cpu,
     }
