@@ -149,6 +149,8 @@ def test_kimi_shape_batch_zipf():
     for t in sample:
         one = _run(bank, x[t:t + 1].contiguous(), ids[t:t + 1].copy(), w[t:t + 1].copy())
         _check(one, got[t:t + 1])
+    # a second launch may place an expert's entries in another order (the grouping takes
+    # places from counting atomics); the output must not change
     again = _run(bank, x, ids, w)
     assert np.array_equal(again, got)
 
